@@ -1,0 +1,194 @@
+/*
+ * nanotitan_moe.h — C ABI of the MI355X (gfx950) MoE expert path.
+ *
+ * One shared library, libnanotitan_moe.so, built by hipcc for gfx950. Every
+ * entry point takes plain device pointers, sizes and a hipStream_t; launches
+ * are stream-ordered, never synchronise the host and never allocate. Outputs
+ * and the workspace are owned by the caller. Each call returns NT_OK or an
+ * NT_ERR_* code; nt_strerror() turns a code into a message.
+ *
+ * Element types: activations/weights are NT_F32, NT_F64, NT_F16 or NT_BF16
+ * (the four float types the reference dispatches over); gates are float32;
+ * token ids, expert ids, offsets and cursors are int32. All matrices are
+ * row-major and contiguous.
+ *
+ * Packed order ("canonical order"): assignment f = t*k + j (token t, slot j)
+ * with expert e = topk[f] lands at
+ *     p(f) = base[e] + #{ f' < f : topk[f'] == e }
+ * i.e. a stable counting sort of the flat assignment index by expert. The
+ * reference's atomic-cursor kernel leaves the order inside an expert segment
+ * unspecified; its torch backend produces exactly this order
+ * (src/model/torch_backend.py:58-66).
+ *
+ * Reference interfaces replaced (paths relative to the nanoTitan tree):
+ *   csrc/bindings.cpp:9,63      count_expert_kernel       -> nt_count_experts
+ *   csrc/bindings.cpp:17-22,64  pack_tokens_kernel        -> nt_pack_tokens
+ *   csrc/bindings.cpp:10-16,66  combine_tokens_kernel     -> nt_combine_tokens
+ *   csrc/bindings.cpp:24-30,67  combine_kernel_backward   -> nt_combine_backward
+ *   csrc/bindings.cpp:32-38,80  pack_kernel_backward      -> nt_pack_backward
+ *   csrc/bindings.cpp:43-47,82  grouped_gemm_kernel       -> nt_grouped_gemm
+ *   csrc/bindings.cpp:53-57,88  bwd_grouped_gemm_dX_kernel-> nt_grouped_gemm_dx
+ *   csrc/bindings.cpp:48-52,84  bwd_grouped_gemm_dW_kernel-> nt_grouped_gemm_dw
+ * plus the torch glue of src/model/cuda_backend.py:46-67 (count, cumsum,
+ * pack) fused into nt_dispatch, and inverse-map variants of combine and pack
+ * backward used by the MoE layer.
+ */
+#ifndef NANOTITAN_MOE_H
+#define NANOTITAN_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum nt_dtype { NT_F32 = 0, NT_F64 = 1, NT_F16 = 2, NT_BF16 = 3 };
+
+/* Return codes. */
+enum nt_status {
+  NT_OK = 0,
+  NT_ERR_INVALID_ARG = 1,   /* null pointer where one is required, negative size */
+  NT_ERR_DTYPE = 2,         /* unknown dtype code */
+  NT_ERR_TOO_MANY_EXPERTS = 3, /* E above NT_MAX_EXPERTS */
+  NT_ERR_WORKSPACE = 4,     /* workspace missing or smaller than *_workspace_bytes() */
+  NT_ERR_LAUNCH = 5,        /* a kernel launch failed (hipGetLastError) */
+  NT_ERR_TOO_LARGE = 6      /* a size exceeds what the kernels index (e.g. > 2^31-1 rows) */
+};
+
+#define NT_MAX_EXPERTS 1024
+
+/* Message for a status code (static storage). */
+const char* nt_strerror(int code);
+
+/* Library version, major*10000 + minor*100 + patch. */
+int nt_version(void);
+
+/* ------------------------------------------------------------------ dispatch */
+
+/* Workspace for nt_count_experts / nt_pack_tokens / nt_dispatch with these
+ * sizes (per-block expert histograms and bases). */
+size_t nt_dispatch_workspace_bytes(int64_t T, int32_t k, int32_t E, int64_t d, int dtype);
+
+/* counts[e] = #{ (t,j) : mask[t] != 0 and topk[t*k+j] == e }.
+ * topk [T,k] int32, mask [T] int32 or NULL (all tokens count), counts [E].
+ * Ids outside [0,E) are ignored.
+ * Replaces count_expert_kernel (reference csrc/kernels/count_experts.cu:32-57). */
+int nt_count_experts(const int32_t* topk, const int32_t* mask, int64_t T, int32_t k,
+                     int32_t E, int32_t* counts, void* ws, size_t ws_bytes,
+                     hipStream_t stream);
+
+/* Pack token rows into expert-major order.
+ * Inputs:  X [T,d] (dtype), w [T,k] f32, topk [T,k] i32,
+ *          cursor [E+1] i32: cursor[e] is the first packed slot of expert e.
+ * Outputs: packed_X [A_cap,d], token_id [A_cap], expert [A_cap],
+ *          packed_w [A_cap] (A_cap = T*k), and inv [T*k] (may be NULL):
+ *          inv[f] = packed slot of assignment f, or -1 if it was dropped.
+ * Slot of assignment f: cursor[e] + #{ f' < f : topk[f'] == e } (canonical
+ * order). On return cursor[e] += count[e] for e < E, the post-state the
+ * reference's atomic cursor leaves. Assignments with ids outside [0,E) or a
+ * slot outside [0,A_cap) are dropped (their rows are not written).
+ * Replaces pack_tokens_kernel (reference csrc/kernels/pack_tokens.cu:51-111). */
+int nt_pack_tokens(int dtype, const void* X, const float* w, const int32_t* topk,
+                   int64_t T, int32_t k, int64_t d, int32_t E, int32_t* cursor,
+                   void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                   int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Fused count + exclusive scan + pack (the glue of reference
+ * src/model/cuda_backend.py:46-67 plus pack_tokens_kernel):
+ * counts [E], offsets [E+1] (offsets[0] = 0, offsets[e+1] = offsets[e] +
+ * counts[e]), then the canonical pack with base = offsets. Outputs as in
+ * nt_pack_tokens; inv may be NULL. */
+int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------- combine */
+
+/* Workspace for the token-id (CSR) forms of combine and pack backward. */
+size_t nt_combine_workspace_bytes(int64_t A, int64_t T);
+
+/* out[t,:] = sum over packed rows p with token_id[p] == t, in ascending p, of
+ * fl32(w[p] * float(y[p,:])), accumulated in float32 without fused
+ * multiply-add. y [A,d] (dtype), token_id [A], w [A] f32, out [T,d] f32.
+ * Tokens with no rows get 0. Ids outside [0,T) are ignored.
+ * Replaces combine_tokens_kernel (reference csrc/kernels/combine_kernels.cu:36-78). */
+int nt_combine_tokens(int dtype, const void* y, const int32_t* token_id, const float* w,
+                      int64_t A, int64_t T, int64_t d, float* out, void* ws,
+                      size_t ws_bytes, hipStream_t stream);
+
+/* Same sum driven by the inverse map of nt_pack_tokens: the rows of token t
+ * are inv[t*k .. t*k+k-1] (entries < 0 skipped), taken in ascending p, so
+ * the result is bit-identical to nt_combine_tokens on the same pack.
+ * out_dtype selects the output element type (NT_F32 for the reference
+ * surface; the activation dtype folds the layer's cast into the kernel). */
+int nt_combine_inv(int dtype, const void* y, const int32_t* inv, const float* w, int64_t T,
+                   int32_t k, int64_t d, int out_dtype, void* out, hipStream_t stream);
+
+/* dy[p,:] = cast(dY[t,:] * w[p]) and dw[p] = sum_h dY[t,h] * float(y[p,h])
+ * with t = token_id[p]; dY [T,d] f32, dy [A,d] (dtype), dw [A] f32.
+ * Rows with an id outside [0,T) get dy = 0, dw = 0.
+ * Replaces combine_kernel_backward (reference csrc/kernels/backward_combine_kernel.cu:42-93). */
+int nt_combine_backward(int dtype, const void* y, const int32_t* token_id, const float* w,
+                        const float* dY, int64_t A, int64_t T, int64_t d, void* dy,
+                        float* dw, hipStream_t stream);
+
+/* Combine backward driven by the inverse map: one pass per token reads its
+ * dY row once. dY_dtype is NT_F32 or the activation dtype. */
+int nt_combine_backward_inv(int dtype, const void* y, const int32_t* inv, const float* w,
+                            int dY_dtype, const void* dY, int64_t T, int32_t k, int64_t d,
+                            void* dy, float* dw, hipStream_t stream);
+
+/* dX[t,:] = cast(sum over p with token_id[p] == t, ascending p, of float(dpX[p,:]));
+ * dw[t,j] = sum of dpw[p] over those p whose expert[p] first matches topk[t,j]
+ * (j = the lowest slot with topk[t,j] == expert[p]; rows with no match add
+ * nothing). dpX [A,d], dpw [A] f32, token_id/expert [A], topk [T,k],
+ * dX [T,d] (dtype), dw [T,k] f32.
+ * Replaces pack_kernel_backward (reference csrc/kernels/backward_pack_kernel.cu:46-101). */
+int nt_pack_backward(int dtype, const void* dpX, const float* dpw, const int32_t* token_id,
+                     const int32_t* expert, const int32_t* topk, int64_t A, int64_t T,
+                     int32_t k, int64_t d, void* dX, float* dw, void* ws, size_t ws_bytes,
+                     hipStream_t stream);
+
+/* Pack backward driven by the inverse map: dX[t,:] = cast(sum of dpX rows
+ * inv[t*k+j] in ascending slot order), dw[t,j] = dpw[inv[t*k+j]] (0 when
+ * inv < 0). */
+int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int32_t* inv,
+                         int64_t T, int32_t k, int64_t d, void* dX, float* dw,
+                         hipStream_t stream);
+
+/* ------------------------------------------------------------- grouped GEMM */
+
+/* Workspace for the grouped GEMMs (dW split-K partials and tile schedule). */
+size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N);
+
+/* out[a,:] = X[a,:] @ W[e] for a in [offsets[e], offsets[e+1]), float32
+ * accumulation, cast to dtype. X [A,K], W [E,K,N], out [A,N], offsets [E+1]
+ * non-decreasing with offsets[E] <= A. Rows >= offsets[E] are not written.
+ * Replaces grouped_gemm_kernel (reference csrc/kernels/grouped_gemm.cu:43-91). */
+int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void* W, int32_t E,
+                    int64_t A, int64_t K, int64_t N, void* out, void* ws, size_t ws_bytes,
+                    hipStream_t stream);
+
+/* dX[a,:] = dOut[a,:] @ W[e]^T. W [E,K,N], dOut [A,N], dX [A,K].
+ * Replaces bwd_grouped_gemm_dX_kernel (reference csrc/kernels/bwd_grouped_gemm_dX.cu:46-96). */
+int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                       int32_t E, int64_t A, int64_t K, int64_t N, void* dX, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+
+/* dW[e] = X_e^T @ dOut_e summed over the rows of expert e (zero for an empty
+ * expert). X [A,K], dOut [A,N], dW [E,K,N]. Deterministic: fixed split of
+ * each expert's rows, partials reduced in a fixed order.
+ * Replaces bwd_grouped_gemm_dW_kernel (reference csrc/kernels/bwd_grouped_gemm_dW.cu:43-86). */
+int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
+                       int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
+                       size_t ws_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOTITAN_MOE_H */

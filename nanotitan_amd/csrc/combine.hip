@@ -1,0 +1,642 @@
+// Weighted combine (forward and backward) and pack backward for gfx950.
+//
+// All three are per-token gathers: one wave owns one token, takes the packed
+// rows that belong to it in ascending packed index, and accumulates in fp32
+// in that fixed order. No floating-point atomics, so results are identical
+// run to run, and the combine equals a sequential index_add_ in packed
+// order bit for bit (products are rounded before the add: no FMA).
+//
+// The rows of a token come either from the inverse map written by the pack
+// (inv[t*k + j] = packed slot of token t's j-th choice) or, on the
+// reference's token-id surface, from a token CSR built here: count rows per
+// token, exclusive scan, fill. The fill claims slots with integer atomics, so
+// each token's list is sorted in LDS before use (lists of up to kMaxSorted
+// rows; a longer list is summed in fill order).
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace nt {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxSorted = 256;
+
+template <typename S, int N>
+struct alignas(sizeof(S) * N) vpack {
+  S v[N];
+};
+
+// VE consecutive elements of type T, as floats.
+template <typename T, int VE>
+__device__ __forceinline__ void load_vec(const typename elem<T>::storage* p, float (&out)[VE]) {
+  using S = typename elem<T>::storage;
+  const vpack<S, VE> v = *reinterpret_cast<const vpack<S, VE>*>(p);
+#pragma unroll
+  for (int i = 0; i < VE; ++i) out[i] = elem<T>::load(v.v[i]);
+}
+
+template <typename T, int VE>
+__device__ __forceinline__ void store_vec(typename elem<T>::storage* p, const float (&in)[VE]) {
+  using S = typename elem<T>::storage;
+  vpack<S, VE> v;
+#pragma unroll
+  for (int i = 0; i < VE; ++i) v.v[i] = elem<T>::store(in[i]);
+  *reinterpret_cast<vpack<S, VE>*>(p) = v;
+}
+
+// ----------------------------------------------------------- token lists
+
+// List source: either CSR (start[t], start[t+1]) into `list`, or the inverse
+// map (t*k .. t*k+k) of `inv`.
+struct ListSrc {
+  const int32_t* start;  // [T+1] or nullptr
+  const int32_t* list;   // CSR entries or inv
+  int32_t k;             // used when start == nullptr
+  int64_t rows;          // packed rows; entries outside [0, rows) are skipped
+};
+
+// Gathers the packed rows of token t into s_out (wave-private LDS of
+// kMaxSorted ints) in ascending order and returns their count, or, for a list
+// longer than kMaxSorted, returns -(length) and leaves the caller to walk it
+// unsorted.
+__device__ int gather_sorted(const ListSrc& src, int64_t t, int32_t* s_in, int32_t* s_out,
+                             int64_t* first) {
+  const int lane = lane_id();
+  int64_t b, n;
+  if (src.start != nullptr) {
+    b = src.start[t];
+    n = src.start[t + 1] - b;
+  } else {
+    b = t * src.k;
+    n = src.k;
+  }
+  *first = b;
+  if (n > kMaxSorted) return -(int)n;
+  // Compact valid (>= 0) entries into s_in.
+  int cnt = 0;
+  for (int64_t base = 0; base < n; base += kWave) {
+    const int64_t i = base + lane;
+    const int32_t p = i < n ? src.list[b + i] : -1;
+    const bool ok = p >= 0 && p < src.rows;
+    const uint64_t m = ballot(ok);
+    if (ok) s_in[cnt + popc64(m & lanemask_lt())] = p;
+    cnt += popc64(m);
+  }
+  lds_wave_sync();
+  // Rank each entry (ties broken by position, so the ranks form a permutation).
+  for (int i = lane; i < cnt; i += kWave) {
+    const int32_t pi = s_in[i];
+    int r = 0;
+    for (int m = 0; m < cnt; ++m) {
+      const int32_t pm = s_in[m];
+      r += (pm < pi) || (pm == pi && m < i);
+    }
+    s_out[r] = pi;
+  }
+  lds_wave_sync();
+  return cnt;
+}
+
+__device__ __forceinline__ int32_t list_entry(const ListSrc& src, const int32_t* s_sorted, int n,
+                                              int64_t first, int i) {
+  if (n >= 0) return s_sorted[i];
+  const int32_t p = src.list[first + i];
+  return p < src.rows ? p : -1;
+}
+
+// --------------------------------------------------------- CSR building
+
+__global__ void zero_i32(int32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+__global__ void token_count_kernel(const int32_t* __restrict__ token_id, int64_t A, int64_t T,
+                                   int32_t* __restrict__ cnt) {
+  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < A;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t t = token_id[p];
+    if (t >= 0 && t < T) atomicAdd(&cnt[t], 1);
+  }
+}
+
+// One workgroup of 1024 threads: start[0..T] = exclusive scan of cnt; cnt is
+// reset to zero for reuse as the fill cursor.
+__global__ void __launch_bounds__(1024)
+token_scan_kernel(int32_t* __restrict__ cnt, int64_t T, int32_t* __restrict__ start) {
+  __shared__ int32_t s_wsum[16];
+  __shared__ int32_t s_carry;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (int64_t s = 0; s < T; s += 1024) {
+    const int64_t i = s + threadIdx.x;
+    const int v = i < T ? cnt[i] : 0;
+    const int incl = wave_incl_scan(v);
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    int before = s_carry;
+    for (int w = 0; w < wave; ++w) before += s_wsum[w];
+    if (i < T) {
+      start[i] = before + incl - v;
+      cnt[i] = 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int tot = 0;
+      for (int w = 0; w < 16; ++w) tot += s_wsum[w];
+      s_carry += tot;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) start[T] = s_carry;
+}
+
+__global__ void token_fill_kernel(const int32_t* __restrict__ token_id, int64_t A, int64_t T,
+                                  const int32_t* __restrict__ start, int32_t* __restrict__ cur,
+                                  int32_t* __restrict__ list) {
+  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < A;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t t = token_id[p];
+    if (t >= 0 && t < T) {
+      const int slot = atomicAdd(&cur[t], 1);
+      list[start[t] + slot] = (int32_t)p;
+    }
+  }
+}
+
+struct CsrWs {
+  int32_t* cnt;    // [T]
+  int32_t* start;  // [T+1]
+  int32_t* list;   // [A]
+};
+
+CsrWs carve_csr(void* ws, int64_t A, int64_t T) {
+  char* c = static_cast<char*>(ws);
+  CsrWs r;
+  r.cnt = reinterpret_cast<int32_t*>(c);
+  c += round_up(T * 4, 256);
+  r.start = reinterpret_cast<int32_t*>(c);
+  c += round_up((T + 1) * 4, 256);
+  r.list = reinterpret_cast<int32_t*>(c);
+  return r;
+}
+
+size_t csr_bytes(int64_t A, int64_t T) {
+  return (size_t)(round_up(T * 4, 256) + round_up((T + 1) * 4, 256) + round_up(A * 4, 256));
+}
+
+int build_csr(const int32_t* token_id, int64_t A, int64_t T, const CsrWs& c, hipStream_t s) {
+  const int grid_t = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(T, 1), 256), 4096);
+  const int grid_a = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(A, 1), 256), 4096);
+  hipLaunchKernelGGL(zero_i32, dim3(grid_t), dim3(256), 0, s, c.cnt, T);
+  hipLaunchKernelGGL(token_count_kernel, dim3(grid_a), dim3(256), 0, s, token_id, A, T, c.cnt);
+  hipLaunchKernelGGL(token_scan_kernel, dim3(1), dim3(1024), 0, s, c.cnt, T, c.start);
+  hipLaunchKernelGGL(token_fill_kernel, dim3(grid_a), dim3(256), 0, s, token_id, A, T, c.start,
+                     c.cnt, c.list);
+  return launch_status();
+}
+
+// ------------------------------------------------------------- combine fwd
+
+// out[t, :] = sum_{p in rows(t), ascending} fl(w[p] * float(y[p, :])).
+template <typename T, typename TO, int VE>
+__global__ void __launch_bounds__(kThreads)
+combine_kernel(const typename elem<T>::storage* __restrict__ y, ListSrc src,
+               const float* __restrict__ w, int64_t T_, int64_t d,
+               typename elem<TO>::storage* __restrict__ out) {
+  __shared__ int32_t s_lists[kWaves][2][kMaxSorted];
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kWaves + wave;
+  if (t >= T_) return;
+  int64_t first;
+  const int n = gather_sorted(src, t, s_lists[wave][0], s_lists[wave][1], &first);
+  const int nn = n >= 0 ? n : -n;
+  const int32_t* sorted = s_lists[wave][1];
+  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+    float acc[VE];
+#pragma unroll
+    for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+    for (int i = 0; i < nn; ++i) {
+      const int32_t p = list_entry(src, sorted, n, first, i);
+      if (p < 0) continue;
+      const float wp = w[p];
+      float x[VE];
+      load_vec<T, VE>(y + (int64_t)p * d + h, x);
+#pragma unroll
+      for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(wp, x[v]));
+    }
+    store_vec<TO, VE>(out + t * d + h, acc);
+  }
+}
+
+// ------------------------------------------------------------- combine bwd
+
+// Generic form, one wave per packed row p:
+// dy[p,:] = cast(dY[t,:] * w[p]); dw[p] = sum_h dY[t,h] * y[p,h].
+template <typename T, typename TG, int VE>
+__global__ void __launch_bounds__(kThreads)
+combine_bwd_kernel(const typename elem<T>::storage* __restrict__ y,
+                   const int32_t* __restrict__ token_id, const float* __restrict__ w,
+                   const typename elem<TG>::storage* __restrict__ dY, int64_t A, int64_t T_,
+                   int64_t d, typename elem<T>::storage* __restrict__ dy, float* __restrict__ dw) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t p = (int64_t)blockIdx.x * kWaves + wave;
+  if (p >= A) return;
+  const int32_t t = token_id[p];
+  const bool ok = t >= 0 && t < T_;
+  const float wp = w[p];
+  float part = 0.f;
+  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+    float g[VE], x[VE], o[VE];
+    if (ok) {
+      load_vec<TG, VE>(dY + (int64_t)t * d + h, g);
+      load_vec<T, VE>(y + p * d + h, x);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VE; ++v) g[v] = x[v] = 0.f;
+    }
+#pragma unroll
+    for (int v = 0; v < VE; ++v) {
+      o[v] = __fmul_rn(g[v], wp);
+      part = fmaf(g[v], x[v], part);
+    }
+    store_vec<T, VE>(dy + p * d + h, o);
+  }
+  part = wave_sum(part);
+  if (lane == 0) dw[p] = part;
+}
+
+// Inverse-map form, one wave per token: the dY row is read once and serves
+// all k packed rows of the token. Same per-row arithmetic and reduction
+// order as combine_bwd_kernel, so dw and dy are bit-identical to it.
+template <typename T, typename TG, int VE, int KB>
+__global__ void __launch_bounds__(kThreads)
+combine_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ y,
+                       const int32_t* __restrict__ inv, const float* __restrict__ w,
+                       const typename elem<TG>::storage* __restrict__ dY, int64_t T_, int32_t k,
+                       int64_t d, typename elem<T>::storage* __restrict__ dy,
+                       float* __restrict__ dw) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kWaves + wave;
+  if (t >= T_) return;
+  for (int j0 = 0; j0 < k; j0 += KB) {
+    const int nj = min(KB, k - j0);
+    int32_t pj[KB];
+    float wj[KB], part[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      pj[j] = j < nj ? inv[t * k + j0 + j] : -1;
+      if (pj[j] >= T_ * k) pj[j] = -1;
+      wj[j] = pj[j] >= 0 ? w[pj[j]] : 0.f;
+      part[j] = 0.f;
+    }
+    for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+      float g[VE];
+      load_vec<TG, VE>(dY + t * d + h, g);
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        if (pj[j] < 0) continue;
+        float x[VE], o[VE];
+        load_vec<T, VE>(y + (int64_t)pj[j] * d + h, x);
+#pragma unroll
+        for (int v = 0; v < VE; ++v) {
+          o[v] = __fmul_rn(g[v], wj[j]);
+          part[j] = fmaf(g[v], x[v], part[j]);
+        }
+        store_vec<T, VE>(dy + (int64_t)pj[j] * d + h, o);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const float s = wave_sum(part[j]);
+      if (lane == 0 && pj[j] >= 0) dw[pj[j]] = s;
+    }
+  }
+}
+
+// --------------------------------------------------------------- pack bwd
+
+// dX[t,:] = cast(sum over rows(t) ascending of dpX[p,:]).
+// dw: generic form (expert != nullptr): dw[t,j] = sum of dpw[p] for rows p
+// whose expert first matches topk[t,j]; inverse form: dw[t,j] = dpw[inv[t*k+j]].
+template <typename T, int VE>
+__global__ void __launch_bounds__(kThreads)
+pack_bwd_kernel(const typename elem<T>::storage* __restrict__ dpX, const float* __restrict__ dpw,
+                ListSrc src, const int32_t* __restrict__ expert, const int32_t* __restrict__ topk,
+                int64_t T_, int32_t k, int64_t d, typename elem<T>::storage* __restrict__ dX,
+                float* __restrict__ dw) {
+  __shared__ int32_t s_lists[kWaves][2][kMaxSorted];
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kWaves + wave;
+  if (t >= T_) return;
+  int64_t first;
+  const int n = gather_sorted(src, t, s_lists[wave][0], s_lists[wave][1], &first);
+  const int nn = n >= 0 ? n : -n;
+  const int32_t* sorted = s_lists[wave][1];
+  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+    float acc[VE];
+#pragma unroll
+    for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+    for (int i = 0; i < nn; ++i) {
+      const int32_t p = list_entry(src, sorted, n, first, i);
+      if (p < 0) continue;
+      float x[VE];
+      load_vec<T, VE>(dpX + (int64_t)p * d + h, x);
+#pragma unroll
+      for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], x[v]);
+    }
+    store_vec<T, VE>(dX + t * d + h, acc);
+  }
+  if (expert == nullptr) {
+    // Inverse map: slot j of token t sits at inv[t*k + j].
+    for (int j = lane; j < k; j += kWave) {
+      const int32_t p = src.list[t * k + j];
+      dw[t * k + j] = (p >= 0 && p < src.rows) ? dpw[p] : 0.f;
+    }
+  } else {
+    // Reference rule (csrc/kernels/backward_pack_kernel.cu:35-42): the first
+    // slot whose expert matches receives the row's gate gradient. Lane j
+    // owns slot j and sums its rows in ascending packed order.
+    for (int j = lane; j < k; j += kWave) {
+      const int32_t ej = topk[t * k + j];
+      float acc = 0.f;
+      for (int i = 0; i < nn; ++i) {
+        const int32_t p = list_entry(src, sorted, n, first, i);
+        if (p < 0) continue;
+        const int32_t e = expert[p];
+        if (e != ej) continue;
+        int jf = 0;
+        while (topk[t * k + jf] != e) ++jf;  // terminates: slot j matches
+        if (jf == j) acc = __fadd_rn(acc, dpw[p]);
+      }
+      dw[t * k + j] = acc;
+    }
+  }
+}
+
+// ------------------------------------------------------------- dispatchers
+
+template <typename T>
+int vec_width(int64_t d, const void* a, const void* b, const void* c) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(c);
+  const int eb = (int)sizeof(typename elem<T>::storage);
+  const int max_ve = 16 / eb;
+  for (int ve = max_ve; ve > 1; ve >>= 1) {
+    if (d % ve == 0 && al % (uintptr_t)(ve * eb) == 0) return ve;
+  }
+  return 1;
+}
+
+template <typename T, typename TO>
+int run_combine(const void* y, ListSrc src, const float* w, int64_t T_, int64_t d, void* out,
+                hipStream_t s) {
+  if (T_ == 0) return NT_OK;
+  using S = typename elem<T>::storage;
+  using SO = typename elem<TO>::storage;
+  const dim3 grid((unsigned)ceil_div(T_, kWaves));
+  const int ve = std::min(vec_width<T>(d, y, y, y), vec_width<TO>(d, out, out, out));
+  const S* yp = static_cast<const S*>(y);
+  SO* op = static_cast<SO*>(out);
+  switch (ve) {
+    case 8: hipLaunchKernelGGL((combine_kernel<T, TO, 8>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
+    case 4: hipLaunchKernelGGL((combine_kernel<T, TO, 4>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
+    case 2: hipLaunchKernelGGL((combine_kernel<T, TO, 2>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
+    default: hipLaunchKernelGGL((combine_kernel<T, TO, 1>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
+  }
+  return launch_status();
+}
+
+template <typename T>
+int combine_out_dispatch(int out_dtype, const void* y, ListSrc src, const float* w, int64_t T_,
+                         int64_t d, void* out, hipStream_t s) {
+  switch (out_dtype) {
+    case NT_F32: return run_combine<T, float>(y, src, w, T_, d, out, s);
+    case NT_F64: return run_combine<T, double>(y, src, w, T_, d, out, s);
+    case NT_F16: return run_combine<T, f16>(y, src, w, T_, d, out, s);
+    case NT_BF16: return run_combine<T, bf16>(y, src, w, T_, d, out, s);
+    default: return NT_ERR_DTYPE;
+  }
+}
+
+int combine_dispatch(int dtype, int out_dtype, const void* y, ListSrc src, const float* w,
+                     int64_t T_, int64_t d, void* out, hipStream_t s) {
+  switch (dtype) {
+    case NT_F32: return combine_out_dispatch<float>(out_dtype, y, src, w, T_, d, out, s);
+    case NT_F64: return combine_out_dispatch<double>(out_dtype, y, src, w, T_, d, out, s);
+    case NT_F16: return combine_out_dispatch<f16>(out_dtype, y, src, w, T_, d, out, s);
+    case NT_BF16: return combine_out_dispatch<bf16>(out_dtype, y, src, w, T_, d, out, s);
+    default: return NT_ERR_DTYPE;
+  }
+}
+
+template <typename T, typename TG>
+int run_combine_bwd(const void* y, const int32_t* token_id, const float* w, const void* dY,
+                    int64_t A, int64_t T_, int64_t d, void* dy, float* dw, hipStream_t s) {
+  if (A == 0) return NT_OK;
+  using S = typename elem<T>::storage;
+  using SG = typename elem<TG>::storage;
+  const dim3 grid((unsigned)ceil_div(A, kWaves));
+  const int ve = std::min(vec_width<T>(d, y, dy, dy), vec_width<TG>(d, dY, dY, dY));
+  const S* yp = static_cast<const S*>(y);
+  const SG* gp = static_cast<const SG*>(dY);
+  S* dyp = static_cast<S*>(dy);
+  switch (ve) {
+    case 8: hipLaunchKernelGGL((combine_bwd_kernel<T, TG, 8>), grid, dim3(kThreads), 0, s, yp, token_id, w, gp, A, T_, d, dyp, dw); break;
+    case 4: hipLaunchKernelGGL((combine_bwd_kernel<T, TG, 4>), grid, dim3(kThreads), 0, s, yp, token_id, w, gp, A, T_, d, dyp, dw); break;
+    case 2: hipLaunchKernelGGL((combine_bwd_kernel<T, TG, 2>), grid, dim3(kThreads), 0, s, yp, token_id, w, gp, A, T_, d, dyp, dw); break;
+    default: hipLaunchKernelGGL((combine_bwd_kernel<T, TG, 1>), grid, dim3(kThreads), 0, s, yp, token_id, w, gp, A, T_, d, dyp, dw); break;
+  }
+  return launch_status();
+}
+
+template <typename T, typename TG>
+int run_combine_bwd_inv(const void* y, const int32_t* inv, const float* w, const void* dY,
+                        int64_t T_, int32_t k, int64_t d, void* dy, float* dw, hipStream_t s) {
+  if (T_ == 0) return NT_OK;
+  using S = typename elem<T>::storage;
+  using SG = typename elem<TG>::storage;
+  const dim3 grid((unsigned)ceil_div(T_, kWaves));
+  const int ve = std::min(vec_width<T>(d, y, dy, dy), vec_width<TG>(d, dY, dY, dY));
+  const S* yp = static_cast<const S*>(y);
+  const SG* gp = static_cast<const SG*>(dY);
+  S* dyp = static_cast<S*>(dy);
+#define NT_CBI(VE, KB) \
+  hipLaunchKernelGGL((combine_bwd_inv_kernel<T, TG, VE, KB>), grid, dim3(kThreads), 0, s, yp, inv, w, gp, T_, k, d, dyp, dw)
+  if (k <= 2) {
+    switch (ve) {
+      case 8: NT_CBI(8, 2); break;
+      case 4: NT_CBI(4, 2); break;
+      case 2: NT_CBI(2, 2); break;
+      default: NT_CBI(1, 2); break;
+    }
+  } else {
+    switch (ve) {
+      case 8: NT_CBI(8, 8); break;
+      case 4: NT_CBI(4, 8); break;
+      case 2: NT_CBI(2, 8); break;
+      default: NT_CBI(1, 8); break;
+    }
+  }
+#undef NT_CBI
+  return launch_status();
+}
+
+template <typename T>
+int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* expert,
+                 const int32_t* topk, int64_t T_, int32_t k, int64_t d, void* dX, float* dw,
+                 hipStream_t s) {
+  if (T_ == 0) return NT_OK;
+  using S = typename elem<T>::storage;
+  const dim3 grid((unsigned)ceil_div(T_, kWaves));
+  const int ve = vec_width<T>(d, dpX, dX, dX);
+  const S* ip = static_cast<const S*>(dpX);
+  S* op = static_cast<S*>(dX);
+  switch (ve) {
+    case 8: hipLaunchKernelGGL((pack_bwd_kernel<T, 8>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;
+    case 4: hipLaunchKernelGGL((pack_bwd_kernel<T, 4>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;
+    case 2: hipLaunchKernelGGL((pack_bwd_kernel<T, 2>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;
+    default: hipLaunchKernelGGL((pack_bwd_kernel<T, 1>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;
+  }
+  return launch_status();
+}
+
+int pack_bwd_dispatch(int dtype, const void* dpX, const float* dpw, ListSrc src,
+                      const int32_t* expert, const int32_t* topk, int64_t T_, int32_t k,
+                      int64_t d, void* dX, float* dw, hipStream_t s) {
+  switch (dtype) {
+    case NT_F32: return run_pack_bwd<float>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
+    case NT_F64: return run_pack_bwd<double>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
+    case NT_F16: return run_pack_bwd<f16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
+    case NT_BF16: return run_pack_bwd<bf16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
+    default: return NT_ERR_DTYPE;
+  }
+}
+
+bool sizes_ok(int64_t a, int64_t b, int64_t d) { return a >= 0 && b >= 0 && d >= 0; }
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+size_t nt_combine_workspace_bytes(int64_t A, int64_t T) {
+  if (A < 0 || T < 0) return 0;
+  return csr_bytes(A, T);
+}
+
+int nt_combine_tokens(int dtype, const void* y, const int32_t* token_id, const float* w,
+                      int64_t A, int64_t T, int64_t d, float* out, void* ws, size_t ws_bytes,
+                      hipStream_t stream) {
+  if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
+  if (!sizes_ok(A, T, d)) return NT_ERR_INVALID_ARG;
+  if (A > INT32_MAX || T > INT32_MAX - 1) return NT_ERR_TOO_LARGE;
+  if (T > 0 && d > 0 && out == nullptr) return NT_ERR_INVALID_ARG;
+  if (A > 0 && (y == nullptr || token_id == nullptr || w == nullptr)) return NT_ERR_INVALID_ARG;
+  if (ws == nullptr || ws_bytes < csr_bytes(A, T)) return NT_ERR_WORKSPACE;
+  if (T == 0) return NT_OK;
+  const CsrWs c = carve_csr(ws, A, T);
+  int st = build_csr(token_id, A, T, c, stream);
+  if (st != NT_OK) return st;
+  ListSrc src{c.start, c.list, 0, A};
+  return combine_dispatch(dtype, NT_F32, y, src, w, T, d, out, stream);
+}
+
+int nt_combine_inv(int dtype, const void* y, const int32_t* inv, const float* w, int64_t T,
+                   int32_t k, int64_t d, int out_dtype, void* out, hipStream_t stream) {
+  if (dtype_bytes(dtype) == 0 || dtype_bytes(out_dtype) == 0) return NT_ERR_DTYPE;
+  if (!sizes_ok(T, k, d) || k < 1) return NT_ERR_INVALID_ARG;
+  if (T * (int64_t)k > INT32_MAX) return NT_ERR_TOO_LARGE;
+  if (T > 0 && (inv == nullptr || w == nullptr || (d > 0 && (y == nullptr || out == nullptr))))
+    return NT_ERR_INVALID_ARG;
+  ListSrc src{nullptr, inv, k, T * k};
+  return combine_dispatch(dtype, out_dtype, y, src, w, T, d, out, stream);
+}
+
+int nt_combine_backward(int dtype, const void* y, const int32_t* token_id, const float* w,
+                        const float* dY, int64_t A, int64_t T, int64_t d, void* dy, float* dw,
+                        hipStream_t stream) {
+  if (!sizes_ok(A, T, d)) return NT_ERR_INVALID_ARG;
+  if (A > 0 && (token_id == nullptr || w == nullptr || dw == nullptr ||
+                (d > 0 && (y == nullptr || dy == nullptr || dY == nullptr))))
+    return NT_ERR_INVALID_ARG;
+  switch (dtype) {
+    case NT_F32: return run_combine_bwd<float, float>(y, token_id, w, dY, A, T, d, dy, dw, stream);
+    case NT_F64: return run_combine_bwd<double, float>(y, token_id, w, dY, A, T, d, dy, dw, stream);
+    case NT_F16: return run_combine_bwd<f16, float>(y, token_id, w, dY, A, T, d, dy, dw, stream);
+    case NT_BF16: return run_combine_bwd<bf16, float>(y, token_id, w, dY, A, T, d, dy, dw, stream);
+    default: return NT_ERR_DTYPE;
+  }
+}
+
+int nt_combine_backward_inv(int dtype, const void* y, const int32_t* inv, const float* w,
+                            int dY_dtype, const void* dY, int64_t T, int32_t k, int64_t d,
+                            void* dy, float* dw, hipStream_t stream) {
+  if (!sizes_ok(T, k, d) || k < 1) return NT_ERR_INVALID_ARG;
+  if (T * (int64_t)k > INT32_MAX) return NT_ERR_TOO_LARGE;
+  if (T > 0 && (inv == nullptr || w == nullptr || dw == nullptr ||
+                (d > 0 && (y == nullptr || dy == nullptr || dY == nullptr))))
+    return NT_ERR_INVALID_ARG;
+  if (dY_dtype != NT_F32 && dY_dtype != dtype) return NT_ERR_DTYPE;
+  const bool g32 = dY_dtype == NT_F32;
+  switch (dtype) {
+    case NT_F32: return run_combine_bwd_inv<float, float>(y, inv, w, dY, T, k, d, dy, dw, stream);
+    case NT_F64:
+      return g32 ? run_combine_bwd_inv<double, float>(y, inv, w, dY, T, k, d, dy, dw, stream)
+                 : run_combine_bwd_inv<double, double>(y, inv, w, dY, T, k, d, dy, dw, stream);
+    case NT_F16:
+      return g32 ? run_combine_bwd_inv<f16, float>(y, inv, w, dY, T, k, d, dy, dw, stream)
+                 : run_combine_bwd_inv<f16, f16>(y, inv, w, dY, T, k, d, dy, dw, stream);
+    case NT_BF16:
+      return g32 ? run_combine_bwd_inv<bf16, float>(y, inv, w, dY, T, k, d, dy, dw, stream)
+                 : run_combine_bwd_inv<bf16, bf16>(y, inv, w, dY, T, k, d, dy, dw, stream);
+    default: return NT_ERR_DTYPE;
+  }
+}
+
+int nt_pack_backward(int dtype, const void* dpX, const float* dpw, const int32_t* token_id,
+                     const int32_t* expert, const int32_t* topk, int64_t A, int64_t T, int32_t k,
+                     int64_t d, void* dX, float* dw, void* ws, size_t ws_bytes,
+                     hipStream_t stream) {
+  if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
+  if (!sizes_ok(A, T, d) || k < 1) return NT_ERR_INVALID_ARG;
+  if (A > INT32_MAX || T * (int64_t)k > INT32_MAX) return NT_ERR_TOO_LARGE;
+  if (T > 0 && (dw == nullptr || topk == nullptr || (d > 0 && dX == nullptr)))
+    return NT_ERR_INVALID_ARG;
+  if (A > 0 && (token_id == nullptr || expert == nullptr || dpw == nullptr ||
+                (d > 0 && dpX == nullptr)))
+    return NT_ERR_INVALID_ARG;
+  if (ws == nullptr || ws_bytes < csr_bytes(A, T)) return NT_ERR_WORKSPACE;
+  if (T == 0) return NT_OK;
+  const CsrWs c = carve_csr(ws, A, T);
+  int st = build_csr(token_id, A, T, c, stream);
+  if (st != NT_OK) return st;
+  ListSrc src{c.start, c.list, 0, A};
+  return pack_bwd_dispatch(dtype, dpX, dpw, src, expert, topk, T, k, d, dX, dw, stream);
+}
+
+int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int32_t* inv,
+                         int64_t T, int32_t k, int64_t d, void* dX, float* dw,
+                         hipStream_t stream) {
+  if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
+  if (!sizes_ok(T, k, d) || k < 1) return NT_ERR_INVALID_ARG;
+  if (T * (int64_t)k > INT32_MAX) return NT_ERR_TOO_LARGE;
+  if (T > 0 && (inv == nullptr || dpw == nullptr || dw == nullptr ||
+                (d > 0 && (dpX == nullptr || dX == nullptr))))
+    return NT_ERR_INVALID_ARG;
+  ListSrc src{nullptr, inv, k, T * k};
+  return pack_bwd_dispatch(dtype, dpX, dpw, src, nullptr, nullptr, T, k, d, dX, dw, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// Shared device helpers for the gfx950 MoE kernels: element conversions,
+// wave64 primitives, launch/argument checking.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nanotitan_moe.h"
+
+namespace nt {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- elements
+// bf16 and fp16 are carried as raw 16-bit patterns; all arithmetic is fp32.
+
+struct bf16 {
+  uint16_t bits;
+};
+struct f16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even, NaN kept quiet: the rounding torch's .to(bfloat16)
+// performs (c10::BFloat16 round_to_nearest_even).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// v_cvt_f16_f32 rounds to nearest even (the default MODE rounding).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <typename T>
+struct elem;
+
+template <>
+struct elem<float> {
+  using storage = float;
+  __device__ static float load(float v) { return v; }
+  __device__ static float store(float v) { return v; }
+};
+template <>
+struct elem<double> {
+  using storage = double;
+  __device__ static float load(double v) { return static_cast<float>(v); }
+  __device__ static double store(float v) { return static_cast<double>(v); }
+};
+template <>
+struct elem<bf16> {
+  using storage = uint16_t;
+  __device__ static float load(uint16_t v) { return bf16_to_f32(v); }
+  __device__ static uint16_t store(float v) { return f32_to_bf16(v); }
+};
+template <>
+struct elem<f16> {
+  using storage = uint16_t;
+  __device__ static float load(uint16_t v) { return f16_to_f32(v); }
+  __device__ static uint16_t store(float v) { return f32_to_f16(v); }
+};
+
+inline int dtype_bytes(int dtype) {
+  switch (dtype) {
+    case NT_F32: return 4;
+    case NT_F64: return 8;
+    case NT_F16: return 2;
+    case NT_BF16: return 2;
+    default: return 0;
+  }
+}
+
+// ------------------------------------------------------------ wave64 helpers
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+__device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
+
+// Butterfly sum over the 64 lanes; every lane receives the total. The
+// association order is fixed, so the result is run-to-run deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Inclusive prefix sum across the wave (Hillis-Steele).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int u = __shfl_up(v, o, kWave);
+    if (l >= o) v += u;
+  }
+  return v;
+}
+
+// Orders a wave's LDS writes before its later LDS reads by other lanes of the
+// same wave (waits for outstanding LDS operations; no workgroup barrier, so
+// it is safe after lanes or waves have diverged).
+__device__ __forceinline__ void lds_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Round a non-negative size up to a multiple of a.
+__host__ __device__ constexpr int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+__host__ __device__ constexpr int64_t ceil_div(int64_t x, int64_t a) { return (x + a - 1) / a; }
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? NT_OK : NT_ERR_LAUNCH; }
+
+}  // namespace nt

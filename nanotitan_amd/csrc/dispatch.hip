@@ -1,0 +1,397 @@
+// Expert counting and top-k token packing (dispatch) for gfx950.
+//
+// Three stream-ordered launches, no host synchronisation, no atomics on the
+// packed order:
+//   1. hist_kernel   one workgroup per block of TB tokens builds an LDS
+//                    histogram of its assignments over the E experts and
+//                    stores it expert-major: hist[e*nb + b].
+//   2. scan_kernel   one workgroup per expert turns hist[e, :] into an
+//                    exclusive scan over blocks and writes counts[e] (and the
+//                    reference's cursor post-state).
+//   3. pack_rows_kernel  one workgroup per token block ranks its assignments
+//                    within the block (wave64 ballots over the bits of the
+//                    expert id give each lane its same-expert peers; a small
+//                    LDS table carries counts across waves and rounds), adds
+//                    the block's base, then copies every token row once from
+//                    X into its k packed slots with 16-byte accesses.
+// Packed order is the stable counting sort of the flat assignment index by
+// expert: exactly the order of the reference torch backend
+// (src/model/torch_backend.py:58-66), deterministic run to run.
+#include "common.hpp"
+
+namespace nt {
+namespace {
+
+constexpr int kDispatchThreads = 256;
+constexpr int kDispatchWaves = kDispatchThreads / kWave;
+
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// hist[e*nb + b] = #{ assignments of tokens [b*TB, b*TB+TB) with expert e,
+//                     token unmasked }.
+__global__ void __launch_bounds__(kDispatchThreads)
+hist_kernel(const int32_t* __restrict__ topk, const int32_t* __restrict__ mask, int64_t T,
+            int32_t k, int32_t E, int32_t TB, int32_t nb, int32_t* __restrict__ hist) {
+  extern __shared__ int32_t s_hist[];
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) s_hist[e] = 0;
+  __syncthreads();
+  const int64_t tok0 = (int64_t)b * TB;
+  const int64_t ntok = min((int64_t)TB, T - tok0);
+  const int64_t na = ntok * k;
+  const int64_t f0 = tok0 * k;
+  for (int64_t i = threadIdx.x; i < na; i += blockDim.x) {
+    const int32_t e = topk[f0 + i];
+    bool ok = e >= 0 && e < E;
+    if (mask != nullptr) ok = ok && mask[tok0 + i / k] != 0;
+    if (ok) atomicAdd(&s_hist[e], 1);  // integer: order-independent
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[(int64_t)e * nb + b] = s_hist[e];
+}
+
+// Workgroup e: exclusive scan of hist[e, 0..nb) in place, counts[e] = total.
+// With a cursor: base[e] = cursor[e]; cursor[e] += total (the state the
+// reference's atomic cursor is left in, csrc/kernels/pack_tokens.cu:37).
+__global__ void __launch_bounds__(kDispatchThreads)
+scan_kernel(int32_t* __restrict__ hist, int32_t nb, int32_t* __restrict__ counts,
+            int32_t* __restrict__ cursor, int32_t* __restrict__ base) {
+  __shared__ int32_t s_wsum[kDispatchWaves];
+  __shared__ int32_t s_carry;
+  const int e = blockIdx.x;
+  int32_t* h = hist + (int64_t)e * nb;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (int start = 0; start < nb; start += kDispatchThreads) {
+    const int i = start + threadIdx.x;
+    const int v = i < nb ? h[i] : 0;
+    const int incl = wave_incl_scan(v);
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    int before = s_carry;
+    for (int w = 0; w < wave; ++w) before += s_wsum[w];
+    if (i < nb) h[i] = before + incl - v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int tot = 0;
+      for (int w = 0; w < kDispatchWaves; ++w) tot += s_wsum[w];
+      s_carry += tot;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int total = s_carry;
+    if (counts != nullptr) counts[e] = total;
+    if (cursor != nullptr) {
+      const int c = cursor[e];
+      base[e] = c;
+      cursor[e] = c + total;
+    }
+  }
+}
+
+template <typename V>
+__device__ __forceinline__ void copy_row_to_slots(const V* __restrict__ src, V* __restrict__ dst,
+                                                  int64_t nv, const int32_t* slots, int k) {
+  const int lane = lane_id();
+  for (int64_t c = lane; c < nv; c += kWave) {
+    const V v = src[c];
+    for (int j = 0; j < k; ++j) {
+      const int32_t p = slots[j];
+      if (p >= 0) dst[(int64_t)p * nv + c] = v;
+    }
+  }
+}
+
+// Rank, place and copy. base_mode 0: base[e] comes from `base` (cursor copy);
+// base_mode 1: base[e] = exclusive scan of counts (offsets), written to
+// `offsets` by workgroup 0.
+template <typename V>
+__global__ void __launch_bounds__(kDispatchThreads)
+pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
+                 const int32_t* __restrict__ topk, int64_t T, int32_t k, int32_t E,
+                 int32_t nbits, int32_t TB, int32_t nb, int64_t nv, int64_t A_cap,
+                 const int32_t* __restrict__ hist, int base_mode,
+                 const int32_t* __restrict__ base, const int32_t* __restrict__ counts,
+                 int32_t* __restrict__ offsets, V* __restrict__ packed_X,
+                 int32_t* __restrict__ token_id, int32_t* __restrict__ expert,
+                 float* __restrict__ packed_w, int32_t* __restrict__ inv) {
+  extern __shared__ int32_t smem[];
+  int32_t* s_base = smem;                 // [E]
+  int32_t* s_run = s_base + E;            // [E]
+  int32_t* s_wc = s_run + E;              // [waves][E]
+  int32_t* s_pos = s_wc + kDispatchWaves * E;  // [TB*k]
+
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+
+  // Per-expert base of this block.
+  if (base_mode == 0) {
+    for (int e = tid; e < E; e += kDispatchThreads) s_base[e] = base[e];
+  } else {
+    // Exclusive scan of counts over experts (E <= NT_MAX_EXPERTS) in s_base.
+    for (int e = tid; e < E; e += kDispatchThreads) s_base[e] = counts[e];
+    __syncthreads();
+    if (wave == 0) {
+      int carry = 0;
+      for (int s = 0; s < E; s += kWave) {
+        const int e = s + lane;
+        const int v = e < E ? s_base[e] : 0;
+        const int incl = wave_incl_scan(v);
+        if (e < E) s_base[e] = carry + incl - v;
+        carry += __shfl(incl, kWave - 1, kWave);
+      }
+      if (b == 0 && offsets != nullptr) {
+        for (int e = lane; e < E; e += kWave) offsets[e] = s_base[e];
+        if (lane == 0) offsets[E] = carry;
+      }
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < E; e += kDispatchThreads) {
+    s_base[e] += hist[(int64_t)e * nb + b];
+    s_run[e] = 0;
+  }
+  for (int i = tid; i < kDispatchWaves * E; i += kDispatchThreads) s_wc[i] = 0;
+  __syncthreads();
+
+  const int64_t tok0 = (int64_t)b * TB;
+  const int ntok = (int)min((int64_t)TB, T - tok0);
+  const int na = ntok * k;
+  const int64_t f0 = tok0 * k;
+
+  // Stable rank of each assignment among same-expert assignments of the block.
+  for (int r = 0; r < na; r += kDispatchThreads) {
+    const int i = r + tid;
+    int32_t e = i < na ? topk[f0 + i] : -1;
+    const bool valid = e >= 0 && e < E;
+    uint64_t peers = ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool set = valid && ((e >> bit) & 1);
+      const uint64_t bb = ballot(set);
+      peers &= set ? bb : ~bb;
+    }
+    const int rank_w = popc64(peers & lanemask_lt());
+    if (valid && rank_w == 0) s_wc[wave * E + e] = popc64(peers);
+    __syncthreads();
+    if (i < na) {
+      int32_t p = -1;
+      if (valid) {
+        int q = s_run[e] + rank_w;
+        for (int w2 = 0; w2 < wave; ++w2) q += s_wc[w2 * E + e];
+        p = s_base[e] + q;
+        if (p < 0 || (int64_t)p >= A_cap) p = -1;
+      }
+      s_pos[i] = p;
+    }
+    __syncthreads();
+    for (int e2 = tid; e2 < E; e2 += kDispatchThreads) {
+      int add = 0;
+      for (int w2 = 0; w2 < kDispatchWaves; ++w2) {
+        add += s_wc[w2 * E + e2];
+        s_wc[w2 * E + e2] = 0;
+      }
+      s_run[e2] += add;
+    }
+    __syncthreads();
+  }
+
+  // Metadata: one thread per assignment.
+  for (int i = tid; i < na; i += kDispatchThreads) {
+    const int32_t p = s_pos[i];
+    const int64_t f = f0 + i;
+    if (inv != nullptr) inv[f] = p;
+    if (p >= 0) {
+      token_id[p] = (int32_t)(tok0 + i / k);
+      expert[p] = topk[f];
+      packed_w[p] = w[f];
+    }
+  }
+
+  // Rows: each wave copies whole token rows, read once, written k times.
+  if (nv > 0) {
+    for (int t = wave; t < ntok; t += kDispatchWaves) {
+      copy_row_to_slots<V>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);
+    }
+  }
+}
+
+struct PackPlan {
+  int32_t TB;
+  int32_t nb;
+  int64_t row_bytes;
+};
+
+PackPlan plan_pack(int64_t T, int32_t k, int64_t row_bytes) {
+  int32_t tb = 64;
+  if (row_bytes >= 8192) tb = 16;
+  else if (row_bytes >= 4096) tb = 16;
+  else if (row_bytes >= 2048) tb = 32;
+  while (tb > 1 && (int64_t)tb * k > 2048) tb >>= 1;
+  PackPlan p;
+  p.TB = tb;
+  p.nb = (int32_t)ceil_div(T, tb);
+  p.row_bytes = row_bytes;
+  return p;
+}
+
+size_t hist_bytes(const PackPlan& p, int32_t E) {
+  return (size_t)round_up((int64_t)E * p.nb * 4, 256);
+}
+
+size_t dispatch_ws_bytes(const PackPlan& p, int32_t E) {
+  return hist_bytes(p, E) + (size_t)round_up((int64_t)E * 4, 256);
+}
+
+int nbits_for(int32_t E) {
+  int n = 0;
+  while ((1 << n) < E) ++n;
+  return n;
+}
+
+int check_common(int64_t T, int32_t k, int32_t E) {
+  if (T < 0 || k < 1 || E < 1) return NT_ERR_INVALID_ARG;
+  if (E > NT_MAX_EXPERTS) return NT_ERR_TOO_MANY_EXPERTS;
+  if (T * (int64_t)k > INT32_MAX) return NT_ERR_TOO_LARGE;
+  return NT_OK;
+}
+
+size_t pack_lds_bytes(const PackPlan& p, int32_t E, int32_t k) {
+  return (size_t)(2 * E + kDispatchWaves * E + (int64_t)p.TB * k) * 4;
+}
+
+template <typename V>
+int launch_pack_rows(const PackPlan& plan, const void* X, const float* w, const int32_t* topk,
+                     int64_t T, int32_t k, int32_t E, const int32_t* hist, int base_mode,
+                     const int32_t* base, const int32_t* counts, int32_t* offsets,
+                     void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                     int32_t* inv, hipStream_t stream) {
+  const int64_t nv = plan.row_bytes / (int64_t)sizeof(V);
+  const size_t lds = pack_lds_bytes(plan, E, k);
+  hipLaunchKernelGGL(pack_rows_kernel<V>, dim3(plan.nb), dim3(kDispatchThreads), lds, stream,
+                     static_cast<const V*>(X), w, topk, T, k, E, nbits_for(E), plan.TB, plan.nb,
+                     nv, T * k, hist, base_mode, base, counts, offsets, static_cast<V*>(packed_X),
+                     token_id, expert, packed_w, inv);
+  return launch_status();
+}
+
+int pack_rows_dispatch(const PackPlan& plan, const void* X, void* packed_X, const float* w,
+                       const int32_t* topk, int64_t T, int32_t k, int32_t E, const int32_t* hist,
+                       int base_mode, const int32_t* base, const int32_t* counts,
+                       int32_t* offsets, int32_t* token_id, int32_t* expert, float* packed_w,
+                       int32_t* inv, hipStream_t stream) {
+  const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(packed_X) |
+                          static_cast<uintptr_t>(plan.row_bytes);
+  if (align % 16 == 0)
+    return launch_pack_rows<uint4>(plan, X, w, topk, T, k, E, hist, base_mode, base, counts,
+                                   offsets, packed_X, token_id, expert, packed_w, inv, stream);
+  if (align % 8 == 0)
+    return launch_pack_rows<uint2>(plan, X, w, topk, T, k, E, hist, base_mode, base, counts,
+                                   offsets, packed_X, token_id, expert, packed_w, inv, stream);
+  if (align % 4 == 0)
+    return launch_pack_rows<uint32_t>(plan, X, w, topk, T, k, E, hist, base_mode, base, counts,
+                                      offsets, packed_X, token_id, expert, packed_w, inv, stream);
+  if (align % 2 == 0)
+    return launch_pack_rows<uint16_t>(plan, X, w, topk, T, k, E, hist, base_mode, base, counts,
+                                      offsets, packed_X, token_id, expert, packed_w, inv, stream);
+  return launch_pack_rows<uint8_t>(plan, X, w, topk, T, k, E, hist, base_mode, base, counts,
+                                   offsets, packed_X, token_id, expert, packed_w, inv, stream);
+}
+
+int launch_hist_scan(const PackPlan& plan, const int32_t* topk, const int32_t* mask, int64_t T,
+                     int32_t k, int32_t E, int32_t* hist, int32_t* counts, int32_t* cursor,
+                     int32_t* base, hipStream_t stream) {
+  if (plan.nb > 0) {
+    hipLaunchKernelGGL(hist_kernel, dim3(plan.nb), dim3(kDispatchThreads), (size_t)E * 4, stream,
+                       topk, mask, T, k, E, plan.TB, plan.nb, hist);
+    int st = launch_status();
+    if (st != NT_OK) return st;
+  }
+  hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, plan.nb,
+                     counts, cursor, base);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+size_t nt_dispatch_workspace_bytes(int64_t T, int32_t k, int32_t E, int64_t d, int dtype) {
+  if (T < 0 || k < 1 || E < 1 || d < 0) return 0;
+  const PackPlan p = plan_pack(T, k, d * dtype_bytes(dtype));
+  return dispatch_ws_bytes(p, E);
+}
+
+int nt_count_experts(const int32_t* topk, const int32_t* mask, int64_t T, int32_t k, int32_t E,
+                     int32_t* counts, void* ws, size_t ws_bytes, hipStream_t stream) {
+  int st = check_common(T, k, E);
+  if (st != NT_OK) return st;
+  if (counts == nullptr || (T > 0 && topk == nullptr)) return NT_ERR_INVALID_ARG;
+  const PackPlan plan = plan_pack(T, k, 0);
+  if (ws == nullptr || ws_bytes < dispatch_ws_bytes(plan, E)) return NT_ERR_WORKSPACE;
+  return launch_hist_scan(plan, topk, mask, T, k, E, static_cast<int32_t*>(ws), counts, nullptr,
+                          nullptr, stream);
+}
+
+int nt_pack_tokens(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                   int32_t k, int64_t d, int32_t E, int32_t* cursor, void* packed_X,
+                   int32_t* token_id, int32_t* expert, float* packed_w, int32_t* inv, void* ws,
+                   size_t ws_bytes, hipStream_t stream) {
+  int st = check_common(T, k, E);
+  if (st != NT_OK) return st;
+  const int eb = dtype_bytes(dtype);
+  if (eb == 0) return NT_ERR_DTYPE;
+  if (d < 0 || cursor == nullptr) return NT_ERR_INVALID_ARG;
+  if (T > 0 && (X == nullptr && d > 0)) return NT_ERR_INVALID_ARG;
+  if (T > 0 && (w == nullptr || topk == nullptr || token_id == nullptr || expert == nullptr ||
+                packed_w == nullptr || (packed_X == nullptr && d > 0)))
+    return NT_ERR_INVALID_ARG;
+  const PackPlan plan = plan_pack(T, k, d * eb);
+  if (ws == nullptr || ws_bytes < dispatch_ws_bytes(plan, E)) return NT_ERR_WORKSPACE;
+  int32_t* hist = static_cast<int32_t*>(ws);
+  int32_t* base = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + hist_bytes(plan, E));
+  st = launch_hist_scan(plan, topk, nullptr, T, k, E, hist, nullptr, cursor, base, stream);
+  if (st != NT_OK || plan.nb == 0) return st;
+  return pack_rows_dispatch(plan, X, packed_X, w, topk, T, k, E, hist, 0, base, nullptr, nullptr,
+                            token_id, expert, packed_w, inv, stream);
+}
+
+int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w, int32_t* inv,
+                void* ws, size_t ws_bytes, hipStream_t stream) {
+  int st = check_common(T, k, E);
+  if (st != NT_OK) return st;
+  const int eb = dtype_bytes(dtype);
+  if (eb == 0) return NT_ERR_DTYPE;
+  if (d < 0 || counts == nullptr || offsets == nullptr) return NT_ERR_INVALID_ARG;
+  if (T > 0 && (w == nullptr || topk == nullptr || token_id == nullptr || expert == nullptr ||
+                packed_w == nullptr || ((X == nullptr || packed_X == nullptr) && d > 0)))
+    return NT_ERR_INVALID_ARG;
+  const PackPlan plan = plan_pack(T, k, d * eb);
+  if (ws == nullptr || ws_bytes < dispatch_ws_bytes(plan, E)) return NT_ERR_WORKSPACE;
+  int32_t* hist = static_cast<int32_t*>(ws);
+  st = launch_hist_scan(plan, topk, nullptr, T, k, E, hist, counts, nullptr, nullptr, stream);
+  if (st != NT_OK) return st;
+  if (plan.nb == 0) {
+    // No tokens: offsets are all zero.
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(kDispatchThreads), 0, stream, offsets,
+                       (int64_t)E + 1, 0);
+    return launch_status();
+  }
+  return pack_rows_dispatch(plan, X, packed_X, w, topk, T, k, E, hist, 1, nullptr, counts,
+                            offsets, token_id, expert, packed_w, inv, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,574 @@
+// Expert-grouped GEMM forward and its dX / dW gradients for gfx950.
+//
+//   fwd : out[a,:] = X[a,:] @ W[e]          rows a of expert e
+//   dX  : dX[a,:]  = dOut[a,:] @ W[e]^T
+//   dW  : dW[e]    = X_e^T @ dOut_e         reduction over the expert's rows
+//
+// bf16/fp16 with 16-byte-aligned shapes run on the MFMA kernel: 256 threads
+// (4 waves, 2x2), a 128x128 output tile, K staged 64 at a time through LDS in
+// a K-contiguous layout so every MFMA operand is one 16-byte LDS read.
+// Operands that are K-contiguous in HBM (X rows, dOut rows, W rows for dX)
+// are copied straight in; operands that are M/N-contiguous (W for the
+// forward, both operands of dW) are transposed in registers on the way in
+// (4x8 blocks, packed with byte permutes). fp32 accumulation, one
+// round-to-nearest-even cast in the epilogue.
+//
+// A device-side tile scheduler maps the linear workgroup id to (expert,
+// m-tile, n-tile) from the offsets array, so empty experts cost nothing, the
+// host never reads offsets (no .item() syncs) and one launch covers every
+// expert. fp32 / fp64 and shapes that are not multiples of 8 run on a simple
+// LDS-tiled FMA kernel with the same scheduler.
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace nt {
+namespace {
+
+enum GemmMode { kFwd = 0, kDx = 1, kDw = 2 };
+
+constexpr int kGemmThreads = 256;
+
+// ------------------------------------------------------------ scheduling
+
+// Row range of expert e, clamped to [0, A] and made non-decreasing, so a
+// malformed offsets array can never move an access outside the buffers.
+__device__ __forceinline__ void expert_rows(const int32_t* __restrict__ offsets, int e, int64_t A,
+                                            int64_t& r0, int64_t& r1) {
+  int64_t a = offsets[e], b = offsets[e + 1];
+  a = a < 0 ? 0 : (a > A ? A : a);
+  b = b < a ? a : (b > A ? A : b);
+  r0 = a;
+  r1 = b;
+}
+
+// Maps m-tile index `mt_global` (over all experts, expert-major) to its
+// expert. s_pref[e] = number of m-tiles of experts < e; built cooperatively.
+// Returns false when mt_global is past the last tile.
+__device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A, int BM,
+                           int64_t mt_global, int32_t* s_pref, int& e_out, int64_t& r0,
+                           int64_t& r1, int64_t& mt_local) {
+  if (threadIdx.x < kWave) {
+    const int lane = lane_id();
+    int carry = 0;
+    for (int s = 0; s < E; s += kWave) {
+      const int e = s + lane;
+      int v = 0;
+      if (e < E) {
+        int64_t a, b;
+        expert_rows(offsets, e, A, a, b);
+        v = (int)ceil_div(b - a, BM);
+      }
+      const int incl = wave_incl_scan(v);
+      if (e < E) s_pref[e + 1] = carry + incl;
+      carry += __shfl(incl, kWave - 1, kWave);
+    }
+    if (lane == 0) s_pref[0] = 0;
+  }
+  __syncthreads();
+  if (mt_global >= s_pref[E]) return false;
+  int lo = 0, hi = E - 1;  // largest e with s_pref[e] <= mt_global
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt_global) lo = mid;
+    else hi = mid - 1;
+  }
+  // Skip experts with zero tiles that share the same prefix value.
+  while (lo < E - 1 && s_pref[lo + 1] <= mt_global) ++lo;
+  e_out = lo;
+  expert_rows(offsets, lo, A, r0, r1);
+  mt_local = mt_global - s_pref[lo];
+  return true;
+}
+
+// ------------------------------------------------------- MFMA operand tiles
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct mfma_op;
+template <>
+struct mfma_op<bf16> {
+  typedef bf16x8_t vec;
+  __device__ static f32x16_t run(vec a, vec b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct mfma_op<f16> {
+  typedef f16x8_t vec;
+  __device__ static f32x16_t run(vec a, vec b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+constexpr int kLdsStride = kBK + 8;  // elements; 144 B rows keep 16-B reads conflict-free
+
+// K-contiguous operand: element (row, kk) at p[row*ld + kk].
+// One 16-byte chunk (8 elements along kk) per slot.
+template <int ROWS>
+struct LoaderK {
+  static constexpr int kChunks = ROWS * kBK / 8 / kGemmThreads;
+  uint4 r[kChunks];
+  __device__ void load(const uint16_t* __restrict__ p, int64_t ld, int64_t rows_valid,
+                       int64_t k_valid) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int q = threadIdx.x + i * kGemmThreads;
+      const int row = q / (kBK / 8);
+      const int kc = (q % (kBK / 8)) * 8;
+      if (row < rows_valid && kc < k_valid)
+        r[i] = *reinterpret_cast<const uint4*>(p + (int64_t)row * ld + kc);
+      else
+        r[i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  __device__ void store(uint16_t* s) const {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int q = threadIdx.x + i * kGemmThreads;
+      const int row = q / (kBK / 8);
+      const int kc = (q % (kBK / 8)) * 8;
+      *reinterpret_cast<uint4*>(s + row * kLdsStride + kc) = r[i];
+    }
+  }
+};
+
+// M-contiguous operand: element (row, kk) at p[kk*ld + row]. Each slot is a
+// 4 (kk) x 8 (row) block: four 16-byte loads, transposed in registers into
+// eight 8-byte LDS writes (row-major, kk contiguous).
+template <int ROWS>
+struct LoaderM {
+  static constexpr int kBlocks = ROWS * kBK / 32 / kGemmThreads;
+  static_assert(kBlocks >= 1, "tile too small for one 4x8 block per thread");
+  uint4 r[kBlocks][4];
+  __device__ void load(const uint16_t* __restrict__ p, int64_t ld, int64_t rows_valid,
+                       int64_t k_valid) {
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const int q = threadIdx.x + i * kGemmThreads;
+      const int mb = (q % (ROWS / 8)) * 8;
+      const int kb = (q / (ROWS / 8)) * 4;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int kk = kb + rr;
+        if (mb < rows_valid && kk < k_valid)
+          r[i][rr] = *reinterpret_cast<const uint4*>(p + (int64_t)kk * ld + mb);
+        else
+          r[i][rr] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ void store(uint16_t* s) const {
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const int q = threadIdx.x + i * kGemmThreads;
+      const int mb = (q % (ROWS / 8)) * 8;
+      const int kb = (q / (ROWS / 8)) * 4;
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&r[i][0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&r[i][1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&r[i][2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&r[i][3]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // Element 2w: low halves; element 2w+1: high halves.
+        uint2 lo, hi;
+        lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
+        lo.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
+        hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
+        hi.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
+        *reinterpret_cast<uint2*>(s + (mb + 2 * w) * kLdsStride + kb) = lo;
+        *reinterpret_cast<uint2*>(s + (mb + 2 * w + 1) * kLdsStride + kb) = hi;
+      }
+    }
+  }
+};
+
+template <bool KCONTIG, int ROWS>
+struct LoaderSel;
+template <int ROWS>
+struct LoaderSel<true, ROWS> {
+  typedef LoaderK<ROWS> type;
+};
+template <int ROWS>
+struct LoaderSel<false, ROWS> {
+  typedef LoaderM<ROWS> type;
+};
+
+template <typename T>
+__device__ __forceinline__ uint16_t cvt_out(float v) {
+  return elem<T>::store(v);
+}
+
+struct GemmArgs {
+  const void* a;  // fwd: X     dX: dOut   dW: X
+  const void* b;  // fwd: W     dX: W      dW: dOut
+  const int32_t* offsets;
+  int32_t E;
+  int64_t A, K, N;
+  void* out;
+  int32_t ntn;  // output tiles along the n dimension
+  int32_t ntm;  // dW only: output tiles along K
+};
+
+// One 128x128 output tile per workgroup.
+template <typename T, int MODE>
+__global__ void __launch_bounds__(kGemmThreads)
+gg_mfma_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[kBM * kLdsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t s_b[kBN * kLdsStride];
+  __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
+
+  constexpr bool kAK = MODE != kDw;   // A operand K-contiguous?
+  constexpr bool kBK_ = MODE == kDx;  // B operand K-contiguous?
+  typedef typename LoaderSel<kAK, kBM>::type LA;
+  typedef typename LoaderSel<kBK_, kBN>::type LB;
+
+  const uint16_t* pa;
+  const uint16_t* pb;
+  int64_t lda, ldb, rows_valid, cols_valid, kred;
+  uint16_t* po;
+  int64_t ldo;
+
+  const int64_t bid = blockIdx.x;
+  const int nt = (int)(bid % g.ntn);
+  const int64_t mt = bid / g.ntn;
+
+  if (MODE == kDw) {
+    const int e = (int)(mt / g.ntm);
+    const int mtl = (int)(mt % g.ntm);
+    int64_t r0, r1;
+    expert_rows(g.offsets, e, g.A, r0, r1);
+    kred = r1 - r0;
+    pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * kBM;
+    lda = g.K;
+    pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * kBN;
+    ldb = g.N;
+    rows_valid = g.K - (int64_t)mtl * kBM;
+    cols_valid = g.N - (int64_t)nt * kBN;
+    po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * kBM * g.N +
+         (int64_t)nt * kBN;
+    ldo = g.N;
+  } else {
+    int e;
+    int64_t r0, r1, mtl;
+    if (!map_m_tile(g.offsets, g.E, g.A, kBM, mt, s_pref, e, r0, r1, mtl)) return;
+    const int64_t row0 = r0 + mtl * kBM;
+    rows_valid = r1 - row0;
+    if (MODE == kFwd) {
+      pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
+      lda = g.K;
+      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * kBN;
+      ldb = g.N;
+      cols_valid = g.N - (int64_t)nt * kBN;
+      kred = g.K;
+      po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * kBN;
+      ldo = g.N;
+    } else {  // kDx
+      pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
+      lda = g.N;
+      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * kBN * g.N;
+      ldb = g.N;
+      cols_valid = g.K - (int64_t)nt * kBN;
+      kred = g.N;
+      po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * kBN;
+      ldo = g.K;
+    }
+  }
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  LA la;
+  LB lb;
+  const int64_t nk = ceil_div(kred, kBK);
+  // Operand pointers advance along the reduction dimension.
+  const int64_t a_kstep = kAK ? kBK : kBK * lda;
+  const int64_t b_kstep = kBK_ ? kBK : kBK * ldb;
+  if (nk > 0) {
+    la.load(pa, lda, rows_valid, kred);
+    lb.load(pb, ldb, cols_valid, kred);
+  }
+  typedef typename mfma_op<T>::vec vec;
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    la.store(s_a);
+    lb.store(s_b);
+    __syncthreads();
+    if (kt + 1 < nk) {
+      const int64_t kleft = kred - (kt + 1) * kBK;
+      la.load(pa + (kt + 1) * a_kstep, lda, rows_valid, kleft);
+      lb.load(pb + (kt + 1) * b_kstep, ldb, cols_valid, kleft);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      vec av[2], bv[2];
+      const int kof = ks * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[i] = *reinterpret_cast<const vec*>(s_a + (wm * 64 + i * 32 + (lane & 31)) * kLdsStride + kof);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bv[j] = *reinterpret_cast<const vec*>(s_b + (wn * 64 + j * 32 + (lane & 31)) * kLdsStride + kof);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_op<T>::run(av[i], bv[j], acc[i][j]);
+    }
+  }
+
+  // Epilogue: acc[i][j][v] holds C[row][col] with col = lane % 32 and
+  // row = 8*(v/4) + 4*(lane/32) + v%4 inside the 32x32 sub-tile.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int col = wn * 64 + j * 32 + (lane & 31);
+        if (row < rows_valid && col < cols_valid) po[(int64_t)row * ldo + col] = cvt_out<T>(acc[i][j][v]);
+      }
+}
+
+// ------------------------------------------------------- generic FMA kernel
+
+template <typename T>
+struct acc_type {
+  typedef float type;
+};
+template <>
+struct acc_type<double> {
+  typedef double type;
+};
+
+template <typename T>
+__device__ __forceinline__ typename acc_type<T>::type to_acc(typename elem<T>::storage v) {
+  return elem<T>::load(v);
+}
+template <>
+__device__ __forceinline__ double to_acc<double>(double v) {
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ typename elem<T>::storage from_acc(typename acc_type<T>::type v) {
+  return elem<T>::store(v);
+}
+template <>
+__device__ __forceinline__ double from_acc<double>(double v) {
+  return v;
+}
+
+constexpr int kGT = 64;  // generic tile
+constexpr int kGK = 16;
+
+template <typename T, int MODE>
+__global__ void __launch_bounds__(256)
+gg_generic_kernel(GemmArgs g) {
+  typedef typename elem<T>::storage S;
+  typedef typename acc_type<T>::type AT;
+  __shared__ AT s_a[kGK][kGT + 1];
+  __shared__ AT s_b[kGK][kGT + 1];
+  __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
+
+  const S* X = static_cast<const S*>(g.a);
+  const S* Bm = static_cast<const S*>(g.b);
+  S* out = static_cast<S*>(g.out);
+  const int64_t bid = blockIdx.x;
+  const int nt = (int)(bid % g.ntn);
+  const int64_t mt = bid / g.ntn;
+
+  int e;
+  int64_t r0, r1, m0, rows_valid, cols_valid, kred;
+  if (MODE == kDw) {
+    e = (int)(mt / g.ntm);
+    m0 = (mt % g.ntm) * kGT;
+    expert_rows(g.offsets, e, g.A, r0, r1);
+    kred = r1 - r0;
+    rows_valid = g.K - m0;
+    cols_valid = g.N - (int64_t)nt * kGT;
+  } else {
+    int64_t mtl;
+    if (!map_m_tile(g.offsets, g.E, g.A, kGT, mt, s_pref, e, r0, r1, mtl)) return;
+    m0 = r0 + mtl * kGT;
+    rows_valid = r1 - m0;
+    cols_valid = (MODE == kFwd ? g.N : g.K) - (int64_t)nt * kGT;
+    kred = MODE == kFwd ? g.K : g.N;
+  }
+  const int64_t n0 = (int64_t)nt * kGT;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  AT acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0;
+
+  for (int64_t k0 = 0; k0 < kred; k0 += kGK) {
+    for (int q = threadIdx.x; q < kGK * kGT; q += 256) {
+      const int kk = q / kGT, m = q % kGT;
+      const int64_t kg = k0 + kk;
+      AT va = 0, vb = 0;
+      if (kg < kred && m < rows_valid) {
+        if (MODE == kFwd) va = to_acc<T>(X[(m0 + m) * g.K + kg]);
+        else if (MODE == kDx) va = to_acc<T>(X[(m0 + m) * g.N + kg]);
+        else va = to_acc<T>(X[(r0 + kg) * g.K + m0 + m]);
+      }
+      if (kg < kred && m < cols_valid) {
+        const int64_t n = n0 + m;
+        if (MODE == kFwd) vb = to_acc<T>(Bm[(int64_t)e * g.K * g.N + kg * g.N + n]);
+        else if (MODE == kDx) vb = to_acc<T>(Bm[(int64_t)e * g.K * g.N + n * g.N + kg]);
+        else vb = to_acc<T>(Bm[(r0 + kg) * g.N + n]);
+      }
+      s_a[kk][m] = va;
+      s_b[kk][m] = vb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kGK; ++kk) {
+      AT av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = s_a[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = s_b[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = ty * 4 + i, n = tx * 4 + j;
+      if (m < rows_valid && n < cols_valid) {
+        int64_t idx;
+        if (MODE == kFwd) idx = (m0 + m) * g.N + n0 + n;
+        else if (MODE == kDx) idx = (m0 + m) * g.K + n0 + n;
+        else idx = (int64_t)e * g.K * g.N + (m0 + m) * g.N + n0 + n;
+        out[idx] = from_acc<T>(acc[i][j]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------- host side
+
+bool mfma_ok(int dtype, int64_t K, int64_t N, const void* p0, const void* p1, const void* p2) {
+  if (dtype != NT_BF16 && dtype != NT_F16) return false;
+  if (K % 8 != 0 || N % 8 != 0) return false;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p0) | reinterpret_cast<uintptr_t>(p1) |
+                       reinterpret_cast<uintptr_t>(p2);
+  return al % 16 == 0;
+}
+
+template <int MODE>
+int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t s) {
+  const int tile = mfma ? kBM : kGT;
+  const int tile_n = mfma ? kBN : kGT;
+  g.ntn = (int32_t)ceil_div(out_cols, tile_n);
+  int64_t nblocks;
+  if (MODE == kDw) {
+    g.ntm = (int32_t)ceil_div(g.K, tile);
+    nblocks = (int64_t)g.E * g.ntm * g.ntn;
+  } else {
+    g.ntm = 0;
+    nblocks = (ceil_div(g.A, tile) + g.E) * (int64_t)g.ntn;
+  }
+  if (nblocks == 0) return NT_OK;
+  if (nblocks > INT32_MAX) return NT_ERR_TOO_LARGE;
+  const dim3 grid((unsigned)nblocks);
+  if (mfma) {
+    if (dtype == NT_BF16) hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE>), grid, dim3(kGemmThreads), 0, s, g);
+    else hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE>), grid, dim3(kGemmThreads), 0, s, g);
+  } else {
+    switch (dtype) {
+      case NT_F32: hipLaunchKernelGGL((gg_generic_kernel<float, MODE>), grid, dim3(256), 0, s, g); break;
+      case NT_F64: hipLaunchKernelGGL((gg_generic_kernel<double, MODE>), grid, dim3(256), 0, s, g); break;
+      case NT_F16: hipLaunchKernelGGL((gg_generic_kernel<f16, MODE>), grid, dim3(256), 0, s, g); break;
+      case NT_BF16: hipLaunchKernelGGL((gg_generic_kernel<bf16, MODE>), grid, dim3(256), 0, s, g); break;
+      default: return NT_ERR_DTYPE;
+    }
+  }
+  return launch_status();
+}
+
+int check_gemm(int dtype, int32_t E, int64_t A, int64_t K, int64_t N, const void* a,
+               const void* b, const int32_t* offsets, const void* out) {
+  if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
+  if (E < 1 || A < 0 || K < 0 || N < 0) return NT_ERR_INVALID_ARG;
+  if (E > NT_MAX_EXPERTS) return NT_ERR_TOO_MANY_EXPERTS;
+  if (offsets == nullptr) return NT_ERR_INVALID_ARG;
+  if ((A > 0 && K > 0 && a == nullptr) || (K > 0 && N > 0 && b == nullptr)) return NT_ERR_INVALID_ARG;
+  if (out == nullptr && ((A > 0 && (K > 0 || N > 0)) || (K > 0 && N > 0))) return NT_ERR_INVALID_ARG;
+  if (A > INT32_MAX) return NT_ERR_TOO_LARGE;
+  return NT_OK;
+}
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N) {
+  (void)dtype;
+  (void)E;
+  (void)A;
+  (void)K;
+  (void)N;
+  return 0;
+}
+
+int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void* W, int32_t E,
+                    int64_t A, int64_t K, int64_t N, void* out, void* ws, size_t ws_bytes,
+                    hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, X, W, offsets, out);
+  if (st != NT_OK) return st;
+  if (A == 0 || N == 0) return NT_OK;
+  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0};
+  return launch_mode<kFwd>(dtype, g, N, mfma_ok(dtype, K, N, X, W, out), stream);
+}
+
+int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                       int32_t E, int64_t A, int64_t K, int64_t N, void* dX, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
+  if (st != NT_OK) return st;
+  if (A == 0 || K == 0) return NT_OK;
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0};
+  return launch_mode<kDx>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
+}
+
+int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
+                       int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
+  if (st != NT_OK) return st;
+  if (K == 0 || N == 0) return NT_OK;
+  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0};
+  return launch_mode<kDw>(dtype, g, N, mfma_ok(dtype, K, N, X, dOut, dW), stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,415 @@
+// PyTorch-ROCm binding of the MoE expert path.
+//
+// Exposes the eight functions of the reference extension module under their
+// reference names and argument orders (reference csrc/bindings.cpp:6-57,
+// 59-92), plus the fused dispatch and the inverse-map combine/backward used
+// by the HIP MoE layer. Every function validates its tensors (raising
+// RuntimeError like the reference's TORCH_CHECKs), allocates outputs and
+// workspace through torch's caching allocator, and calls the C ABI of
+// libnanotitan_moe.so on the current HIP stream of the input's device. No
+// function synchronises the host.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <tuple>
+
+#include "nanotitan_moe.h"
+
+namespace {
+
+using torch::Tensor;
+
+int dtype_code(const Tensor& t) {
+  switch (t.scalar_type()) {
+    case at::kFloat: return NT_F32;
+    case at::kDouble: return NT_F64;
+    case at::kHalf: return NT_F16;
+    case at::kBFloat16: return NT_BF16;
+    default:
+      TORCH_CHECK(false, "unsupported dtype ", t.scalar_type(),
+                  " (expected float32, float64, float16 or bfloat16)");
+  }
+  return -1;
+}
+
+at::ScalarType scalar_of(int code) {
+  switch (code) {
+    case NT_F32: return at::kFloat;
+    case NT_F64: return at::kDouble;
+    case NT_F16: return at::kHalf;
+    default: return at::kBFloat16;
+  }
+}
+
+void check_status(int st, const char* what) {
+  TORCH_CHECK(st == NT_OK, what, ": ", nt_strerror(st));
+}
+
+void check_device(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+}
+
+void check_i32(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kInt, name, " must be int32");
+  check_device(t, name);
+}
+
+void check_f32(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+  check_device(t, name);
+}
+
+hipStream_t stream_of(const Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+Tensor workspace(const Tensor& like, size_t bytes) {
+  return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
+}
+
+// ------------------------------------------------------ reference surface
+
+// count_expert_kernel(topk_experts_per_token, mask, num_experts, num_topk_experts)
+// reference csrc/kernels/count_experts.cu:32-57.
+Tensor count_expert_kernel(Tensor topk, Tensor mask, int64_t num_experts, int64_t num_topk) {
+  check_i32(topk, "topk_experts_per_token");
+  check_i32(mask, "mask");
+  TORCH_CHECK(topk.is_contiguous() && mask.is_contiguous(), "inputs must be contiguous");
+  TORCH_CHECK(topk.dim() == 2 && topk.size(1) == num_topk,
+              "topk_experts_per_token must be [num_tokens, num_topk_experts]");
+  TORCH_CHECK(mask.numel() == topk.size(0), "mask must have one entry per token");
+  const int64_t T = topk.size(0);
+  c10::hip::HIPGuard guard(topk.get_device());
+  Tensor counts = at::empty({num_experts}, topk.options().dtype(at::kInt));
+  Tensor ws = workspace(topk, nt_dispatch_workspace_bytes(T, (int32_t)num_topk,
+                                                          (int32_t)num_experts, 0, NT_F32));
+  check_status(nt_count_experts(topk.data_ptr<int32_t>(), mask.data_ptr<int32_t>(), T,
+                                (int32_t)num_topk, (int32_t)num_experts, counts.data_ptr<int32_t>(),
+                                ws.data_ptr(), ws.numel(), stream_of(topk)),
+               "count_expert_kernel");
+  return counts;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> pack_impl(Tensor X, Tensor w, Tensor topk,
+                                                             Tensor cursor) {
+  TORCH_CHECK(X.is_contiguous(), "X must be contiguous");
+  TORCH_CHECK(w.is_contiguous(), "topk_weights must be contiguous");
+  check_device(X, "X");
+  check_f32(w, "topk_weights");
+  check_i32(topk, "topk_experts");
+  check_i32(cursor, "expert_offset_cpy");
+  TORCH_CHECK(topk.is_contiguous() && cursor.is_contiguous(), "indices must be contiguous");
+  TORCH_CHECK(X.dim() == 2 && w.dim() == 2 && topk.sizes() == w.sizes() && w.size(0) == X.size(0),
+              "expected X [T,d], topk_weights [T,k], topk_experts [T,k]");
+  TORCH_CHECK(cursor.numel() >= 2, "expert_offset_cpy must hold num_experts + 1 entries");
+  const int64_t T = X.size(0), d = X.size(1), k = w.size(1), A = T * k;
+  const int32_t E = (int32_t)(cursor.numel() - 1);
+  const int dt = dtype_code(X);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor packed_X = at::empty({A, d}, X.options());
+  Tensor token_id = at::empty({A}, X.options().dtype(at::kInt));
+  Tensor expert = at::empty({A}, X.options().dtype(at::kInt));
+  Tensor packed_w = at::empty({A}, X.options().dtype(at::kFloat));
+  Tensor inv = at::empty({T, k}, X.options().dtype(at::kInt));
+  Tensor ws = workspace(X, nt_dispatch_workspace_bytes(T, (int32_t)k, E, d, dt));
+  check_status(nt_pack_tokens(dt, X.data_ptr(), w.data_ptr<float>(), topk.data_ptr<int32_t>(), T,
+                              (int32_t)k, d, E, cursor.data_ptr<int32_t>(), packed_X.data_ptr(),
+                              token_id.data_ptr<int32_t>(), expert.data_ptr<int32_t>(),
+                              packed_w.data_ptr<float>(), inv.data_ptr<int32_t>(), ws.data_ptr(),
+                              ws.numel(), stream_of(X)),
+               "pack_tokens_kernel");
+  return {packed_X, token_id, expert, packed_w, inv};
+}
+
+// pack_tokens_kernel(X, topk_weights, topk_experts, expert_offset_cpy)
+// reference csrc/kernels/pack_tokens.cu:51-111; mutates the cursor like it.
+std::tuple<Tensor, Tensor, Tensor, Tensor> pack_tokens_kernel(Tensor X, Tensor w, Tensor topk,
+                                                              Tensor cursor) {
+  auto r = pack_impl(X, w, topk, cursor);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r)};
+}
+
+// combine_tokens_kernel(expert_outputs, packed_tokenId, packed_topk_weights, num_tokens, d_model)
+// reference csrc/kernels/combine_kernels.cu:36-78. Returns float32 [T, d].
+Tensor combine_tokens_kernel(Tensor y, Tensor token_id, Tensor w, int64_t num_tokens,
+                             int64_t d_model) {
+  TORCH_CHECK(y.is_contiguous(), "Expert output tensor should be contiguous");
+  TORCH_CHECK(token_id.is_contiguous(), "packed token ids tensor should be contiguous");
+  TORCH_CHECK(w.is_contiguous(), "packed topk weights tensor should be contiguous");
+  check_device(y, "expert_outputs");
+  check_i32(token_id, "packed_tokenId");
+  check_f32(w, "packed_topk_weights");
+  TORCH_CHECK(y.dim() == 2 && y.size(1) == d_model, "expert_outputs must be [A, d_model]");
+  TORCH_CHECK(token_id.numel() == y.size(0) && w.numel() == y.size(0),
+              "one token id and one weight per packed row");
+  const int64_t A = y.size(0);
+  c10::hip::HIPGuard guard(y.get_device());
+  Tensor out = at::empty({num_tokens, d_model}, y.options().dtype(at::kFloat));
+  Tensor ws = workspace(y, nt_combine_workspace_bytes(A, num_tokens));
+  check_status(nt_combine_tokens(dtype_code(y), y.data_ptr(), token_id.data_ptr<int32_t>(),
+                                 w.data_ptr<float>(), A, num_tokens, d_model,
+                                 out.data_ptr<float>(), ws.data_ptr(), ws.numel(), stream_of(y)),
+               "combine_tokens_kernel");
+  return out;
+}
+
+// combine_kernel_backward(expert_outputs, packed_tokenIds, packed_topk_weights,
+//                         residual_stream_grad, hidden_dim)
+// reference csrc/kernels/backward_combine_kernel.cu:42-93.
+std::tuple<Tensor, Tensor> combine_kernel_backward(Tensor y, Tensor token_id, Tensor w, Tensor dY,
+                                                   int64_t hidden_dim) {
+  TORCH_CHECK(y.is_contiguous() && token_id.is_contiguous() && w.is_contiguous() &&
+                  dY.is_contiguous(),
+              "Tensor should be laid out in contiguous memory location");
+  TORCH_CHECK(dY.scalar_type() == at::kFloat, "residual_stream_grad must be float32");
+  check_device(y, "expert_outputs");
+  check_device(dY, "residual_stream_grad");
+  check_i32(token_id, "packed_tokenIds");
+  check_f32(w, "packed_topk_weights");
+  TORCH_CHECK(y.dim() == 2 && y.size(1) == hidden_dim && dY.dim() == 2 &&
+                  dY.size(1) == hidden_dim,
+              "expert_outputs and residual_stream_grad must have hidden_dim columns");
+  TORCH_CHECK(token_id.numel() == y.size(0) && w.numel() == y.size(0),
+              "one token id and one weight per packed row");
+  const int64_t A = y.size(0), T = dY.size(0);
+  c10::hip::HIPGuard guard(y.get_device());
+  Tensor dy = at::empty_like(y);
+  Tensor dw = at::empty(w.sizes(), w.options());
+  check_status(nt_combine_backward(dtype_code(y), y.data_ptr(), token_id.data_ptr<int32_t>(),
+                                   w.data_ptr<float>(), dY.data_ptr<float>(), A, T, hidden_dim,
+                                   dy.data_ptr(), dw.data_ptr<float>(), stream_of(y)),
+               "combine_kernel_backward");
+  return {dy, dw};
+}
+
+// pack_kernel_backward(packed_X_grad, packed_topk_weights_grad, packed_tokenId,
+//                      packed_expert, topk_experts)
+// reference csrc/kernels/backward_pack_kernel.cu:46-101.
+std::tuple<Tensor, Tensor> pack_kernel_backward(Tensor dpX, Tensor dpw, Tensor token_id,
+                                                Tensor expert, Tensor topk) {
+  TORCH_CHECK(dpX.is_contiguous(), "packed_X_grad must be contiguous");
+  TORCH_CHECK(dpw.is_contiguous(), "packed_topk_weights_grad must be contiguous");
+  TORCH_CHECK(token_id.is_contiguous(), "packed_tokenId must be contiguous");
+  TORCH_CHECK(expert.is_contiguous(), "packed_expert must be contiguous");
+  TORCH_CHECK(topk.is_contiguous(), "topk_experts must be contiguous");
+  TORCH_CHECK(dpw.scalar_type() == at::kFloat, "packed_topk_weights_grad must be float32");
+  check_device(dpX, "packed_X_grad");
+  check_i32(token_id, "packed_tokenId");
+  check_i32(expert, "packed_expert");
+  check_i32(topk, "topk_experts");
+  TORCH_CHECK(dpX.dim() == 2 && topk.dim() == 2, "expected packed_X_grad [A,d], topk [T,k]");
+  const int64_t A = dpX.size(0), d = dpX.size(1), T = topk.size(0), k = topk.size(1);
+  TORCH_CHECK(dpw.numel() == A && token_id.numel() == A && expert.numel() == A,
+              "one gate grad, token id and expert id per packed row");
+  c10::hip::HIPGuard guard(dpX.get_device());
+  Tensor dX = at::empty({T, d}, dpX.options());
+  Tensor dw = at::empty({T, k}, dpw.options());
+  Tensor ws = workspace(dpX, nt_combine_workspace_bytes(A, T));
+  check_status(nt_pack_backward(dtype_code(dpX), dpX.data_ptr(), dpw.data_ptr<float>(),
+                                token_id.data_ptr<int32_t>(), expert.data_ptr<int32_t>(),
+                                topk.data_ptr<int32_t>(), A, T, (int32_t)k, d, dX.data_ptr(),
+                                dw.data_ptr<float>(), ws.data_ptr(), ws.numel(), stream_of(dpX)),
+               "pack_kernel_backward");
+  return {dX, dw};
+}
+
+void check_gemm_inputs(const Tensor& a, const Tensor& offsets, const Tensor& b) {
+  TORCH_CHECK(a.is_contiguous(), "X must be contiguous");
+  TORCH_CHECK(b.is_contiguous(), "weights must be contiguous");
+  check_device(a, "X");
+  check_device(b, "weights");
+  check_i32(offsets, "expert_offset");
+  TORCH_CHECK(offsets.is_contiguous() && offsets.dim() == 1 && offsets.numel() >= 2,
+              "expert_offset must be a 1-D [num_experts + 1] tensor");
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), "operands must share one dtype");
+}
+
+// grouped_gemm_kernel(X, expert_offset, weights) -> [A, N]
+// reference csrc/kernels/grouped_gemm.cu:43-91.
+Tensor grouped_gemm_kernel(Tensor X, Tensor offsets, Tensor W) {
+  check_gemm_inputs(X, offsets, W);
+  TORCH_CHECK(X.dim() == 2 && W.dim() == 3 && W.size(1) == X.size(1),
+              "expected X [A,K] and weights [E,K,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = X.size(0), K = X.size(1), N = W.size(2);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor out = at::empty({A, N}, X.options());
+  const int dt = dtype_code(X);
+  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm(dt, X.data_ptr(), offsets.data_ptr<int32_t>(), W.data_ptr(), E, A,
+                               K, N, out.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(X)),
+               "grouped_gemm_kernel");
+  return out;
+}
+
+// bwd_grouped_gemm_dW_kernel(X, expert_offset, dOut) -> [E, K, N]
+// reference csrc/kernels/bwd_grouped_gemm_dW.cu:43-86.
+Tensor bwd_grouped_gemm_dW_kernel(Tensor X, Tensor offsets, Tensor dOut) {
+  check_gemm_inputs(X, offsets, dOut);
+  TORCH_CHECK(X.dim() == 2 && dOut.dim() == 2 && dOut.size(0) == X.size(0),
+              "expected X [A,K] and dOut [A,N]");
+  const int64_t A = X.size(0), K = X.size(1), N = dOut.size(1);
+  const int32_t E = (int32_t)(offsets.numel() - 1);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor dW = at::empty({E, K, N}, X.options());
+  const int dt = dtype_code(X);
+  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dw(dt, X.data_ptr(), offsets.data_ptr<int32_t>(), dOut.data_ptr(),
+                                  E, A, K, N, dW.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  stream_of(X)),
+               "bwd_grouped_gemm_dW_kernel");
+  return dW;
+}
+
+// bwd_grouped_gemm_dX_kernel(W_gate, expert_offset, dOut) -> [A, K]
+// reference csrc/kernels/bwd_grouped_gemm_dX.cu:46-96.
+Tensor bwd_grouped_gemm_dX_kernel(Tensor W, Tensor offsets, Tensor dOut) {
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(W.dim() == 3 && dOut.dim() == 2 && dOut.size(1) == W.size(2),
+              "expected W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = dOut.size(0), K = W.size(1), N = W.size(2);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(W.get_device());
+  Tensor dX = at::empty({A, K}, W.options());
+  const int dt = dtype_code(W);
+  Tensor ws = workspace(W, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dx(dt, W.data_ptr(), offsets.data_ptr<int32_t>(), dOut.data_ptr(),
+                                  E, A, K, N, dX.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  stream_of(W)),
+               "bwd_grouped_gemm_dX_kernel");
+  return dX;
+}
+
+// ------------------------------------------------------- layer extensions
+
+// Fused count + scan + pack: (counts [E], offsets [E+1], packed_X, token_id,
+// expert, packed_w, inv [T,k]).
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts) {
+  TORCH_CHECK(X.is_contiguous() && w.is_contiguous() && topk.is_contiguous(),
+              "inputs must be contiguous");
+  check_device(X, "X");
+  check_f32(w, "topk_weights");
+  check_i32(topk, "topk_experts");
+  TORCH_CHECK(X.dim() == 2 && w.dim() == 2 && topk.sizes() == w.sizes() && w.size(0) == X.size(0),
+              "expected X [T,d], topk_weights [T,k], topk_experts [T,k]");
+  const int64_t T = X.size(0), d = X.size(1), k = w.size(1), A = T * k;
+  const int32_t E = (int32_t)num_experts;
+  const int dt = dtype_code(X);
+  c10::hip::HIPGuard guard(X.get_device());
+  auto i32 = X.options().dtype(at::kInt);
+  Tensor counts = at::empty({E}, i32);
+  Tensor offsets = at::empty({E + 1}, i32);
+  Tensor packed_X = at::empty({A, d}, X.options());
+  Tensor token_id = at::empty({A}, i32);
+  Tensor expert = at::empty({A}, i32);
+  Tensor packed_w = at::empty({A}, X.options().dtype(at::kFloat));
+  Tensor inv = at::empty({T, k}, i32);
+  Tensor ws = workspace(X, nt_dispatch_workspace_bytes(T, (int32_t)k, E, d, dt));
+  check_status(nt_dispatch(dt, X.data_ptr(), w.data_ptr<float>(), topk.data_ptr<int32_t>(), T,
+                           (int32_t)k, d, E, counts.data_ptr<int32_t>(),
+                           offsets.data_ptr<int32_t>(), packed_X.data_ptr(),
+                           token_id.data_ptr<int32_t>(), expert.data_ptr<int32_t>(),
+                           packed_w.data_ptr<float>(), inv.data_ptr<int32_t>(), ws.data_ptr(),
+                           ws.numel(), stream_of(X)),
+               "dispatch_tokens");
+  return {counts, offsets, packed_X, token_id, expert, packed_w, inv};
+}
+
+// pack_tokens_kernel plus the inverse map.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> pack_tokens_inv(Tensor X, Tensor w, Tensor topk,
+                                                                   Tensor cursor) {
+  return pack_impl(X, w, topk, cursor);
+}
+
+Tensor combine_inv(Tensor y, Tensor inv, Tensor w, c10::ScalarType out_dtype) {
+  TORCH_CHECK(y.is_contiguous() && inv.is_contiguous() && w.is_contiguous(),
+              "inputs must be contiguous");
+  check_device(y, "expert_outputs");
+  check_i32(inv, "inv");
+  check_f32(w, "packed_topk_weights");
+  TORCH_CHECK(y.dim() == 2 && inv.dim() == 2, "expected y [A,d], inv [T,k]");
+  const int64_t T = inv.size(0), k = inv.size(1), d = y.size(1);
+  c10::hip::HIPGuard guard(y.get_device());
+  Tensor out = at::empty({T, d}, y.options().dtype(out_dtype));
+  Tensor probe = at::empty({0}, y.options().dtype(out_dtype));
+  check_status(nt_combine_inv(dtype_code(y), y.data_ptr(), inv.data_ptr<int32_t>(),
+                              w.data_ptr<float>(), T, (int32_t)k, d, dtype_code(probe),
+                              out.data_ptr(), stream_of(y)),
+               "combine_inv");
+  return out;
+}
+
+std::tuple<Tensor, Tensor> combine_backward_inv(Tensor y, Tensor inv, Tensor w, Tensor dY) {
+  TORCH_CHECK(y.is_contiguous() && inv.is_contiguous() && w.is_contiguous() && dY.is_contiguous(),
+              "inputs must be contiguous");
+  check_device(y, "expert_outputs");
+  check_device(dY, "grad");
+  check_i32(inv, "inv");
+  check_f32(w, "packed_topk_weights");
+  TORCH_CHECK(y.dim() == 2 && inv.dim() == 2 && dY.dim() == 2 && dY.size(0) == inv.size(0) &&
+                  dY.size(1) == y.size(1),
+              "expected y [A,d], inv [T,k], grad [T,d]");
+  TORCH_CHECK(dY.scalar_type() == at::kFloat || dY.scalar_type() == y.scalar_type(),
+              "grad must be float32 or the activation dtype");
+  const int64_t T = inv.size(0), k = inv.size(1), d = y.size(1);
+  c10::hip::HIPGuard guard(y.get_device());
+  Tensor dy = at::empty_like(y);
+  Tensor dw = at::empty(w.sizes(), w.options());
+  check_status(nt_combine_backward_inv(dtype_code(y), y.data_ptr(), inv.data_ptr<int32_t>(),
+                                       w.data_ptr<float>(), dtype_code(dY), dY.data_ptr(), T,
+                                       (int32_t)k, d, dy.data_ptr(), dw.data_ptr<float>(),
+                                       stream_of(y)),
+               "combine_backward_inv");
+  return {dy, dw};
+}
+
+std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv) {
+  TORCH_CHECK(dpX.is_contiguous() && dpw.is_contiguous() && inv.is_contiguous(),
+              "inputs must be contiguous");
+  check_device(dpX, "packed_X_grad");
+  check_f32(dpw, "packed_topk_weights_grad");
+  check_i32(inv, "inv");
+  TORCH_CHECK(dpX.dim() == 2 && inv.dim() == 2, "expected packed_X_grad [A,d], inv [T,k]");
+  const int64_t T = inv.size(0), k = inv.size(1), d = dpX.size(1);
+  c10::hip::HIPGuard guard(dpX.get_device());
+  Tensor dX = at::empty({T, d}, dpX.options());
+  Tensor dw = at::empty({T, k}, dpw.options());
+  check_status(nt_pack_backward_inv(dtype_code(dpX), dpX.data_ptr(), dpw.data_ptr<float>(),
+                                    inv.data_ptr<int32_t>(), T, (int32_t)k, d, dX.data_ptr(),
+                                    dw.data_ptr<float>(), stream_of(dpX)),
+               "pack_backward_inv");
+  return {dX, dw};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "nanoTitan MoE expert path on MI355X (gfx950): HIP kernels behind the reference op surface";
+  m.def("count_expert_kernel", &count_expert_kernel,
+        "Histogram of expert ids over unmasked tokens -> int32 [E]");
+  m.def("pack_tokens_kernel", &pack_tokens_kernel,
+        "[num_tokens, d] -> [num_tokens * k, d] expert-major packing (canonical stable order)");
+  m.def("combine_tokens_kernel", &combine_tokens_kernel,
+        "Gate-weighted sum of packed rows per token -> float32 [T, d]");
+  m.def("combine_kernel_backward", &combine_kernel_backward,
+        "Backward of combine -> (expert_output_grad, packed_topk_weights_grad)");
+  m.def("pack_kernel_backward", &pack_kernel_backward,
+        "Backward of pack -> (X_grad, topk_weights_grad)");
+  m.def("grouped_gemm_kernel", &grouped_gemm_kernel, "Expert-grouped GEMM forward");
+  m.def("bwd_grouped_gemm_dW_kernel", &bwd_grouped_gemm_dW_kernel,
+        "Expert-grouped GEMM weight gradient");
+  m.def("bwd_grouped_gemm_dX_kernel", &bwd_grouped_gemm_dX_kernel,
+        "Expert-grouped GEMM input gradient");
+  m.def("dispatch_tokens", &dispatch_tokens,
+        "Fused count + offsets + pack -> (counts, offsets, packed_X, token_id, expert, packed_w, inv)");
+  m.def("pack_tokens_inv", &pack_tokens_inv, "pack_tokens_kernel that also returns the inverse map");
+  m.def("combine_inv", &combine_inv, "Combine driven by the inverse map");
+  m.def("combine_backward_inv", &combine_backward_inv, "Combine backward driven by the inverse map");
+  m.def("pack_backward_inv", &pack_backward_inv, "Pack backward driven by the inverse map");
+  m.def("version", []() { return nt_version(); });
+}

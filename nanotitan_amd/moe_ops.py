@@ -1,0 +1,197 @@
+"""Autograd surface of the MoE expert path.
+
+Same function names, argument orders and gradient contracts as the
+reference's ``src/model/moe_ops.py:10-125``:
+
+* ``pack_tokens_fn(X, topk_weights, topk_experts, expert_offset_cpy)``
+  -> (packed_X, packed_tokenId, packed_expert, packed_topk_weights);
+  backward returns (X_grad, topk_weights_grad, None, None).
+* ``combine_tokens_fn(packed_expert_outputs, packed_tokenId,
+  packed_topk_weights, num_tokens, hidden_dim)`` -> float32 [T, d];
+  backward casts the incoming grad to float32 contiguous and returns
+  (expert_output_grad, None, packed_topk_weights_grad, None, None).
+* ``grouped_gemm_fn(X, weight, expert_offset)`` applies
+  ``GroupedGEMM_FN.apply(X, expert_offset, weight)``; backward returns
+  (dX, None, dW).
+
+Every op runs the HIP kernels through ``get_hip_extension()``; a missing
+extension raises RuntimeError, never a silent fallback.
+
+The layer uses two additional Functions built on the inverse map the pack
+writes: ``DispatchFN`` (fused count + offsets + pack) and ``CombineInvFN``
+(combine whose backward reads each token's grad row once). They compute the
+same values as pack_tokens_fn / combine_tokens_fn on the same inputs.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from nanotitan_amd.extension import get_hip_extension
+
+
+def combine_tokens_fn(
+    packed_expert_outputs, packed_tokenId, packed_topk_weights, num_tokens, hidden_dim
+):
+    return CombineTokensFN.apply(
+        packed_expert_outputs, packed_tokenId, packed_topk_weights, num_tokens, hidden_dim
+    )
+
+
+def pack_tokens_fn(X, topk_weights, topk_experts, expert_offset_cpy):
+    return PackTokensFN.apply(X, topk_weights, topk_experts, expert_offset_cpy)
+
+
+def grouped_gemm_fn(X, weight, expert_offset):
+    return GroupedGEMM_FN.apply(X, expert_offset, weight)
+
+
+class PackTokensFN(torch.autograd.Function):
+    """Reference: src/model/moe_ops.py:40-73."""
+
+    @staticmethod
+    def forward(ctx, X, topk_weights, topk_experts, expert_offset_cpy) -> tuple:
+        ext = get_hip_extension()
+        packed_X, packed_tokenId, packed_expert, packed_topk_weights = ext.pack_tokens_kernel(
+            X, topk_weights, topk_experts, expert_offset_cpy
+        )
+        ctx.save_for_backward(packed_tokenId, packed_expert, topk_experts)
+        ctx.mark_non_differentiable(packed_tokenId, packed_expert)
+        return packed_X, packed_tokenId, packed_expert, packed_topk_weights
+
+    @staticmethod
+    def backward(ctx, packed_X_grad, packed_tokenId_grad, packed_expert_grad,
+                 packed_topk_weights_grad) -> Any:
+        ext = get_hip_extension()
+        packed_tokenId, packed_expert, topk_experts = ctx.saved_tensors
+        if packed_topk_weights_grad is None:
+            packed_topk_weights_grad = torch.zeros(
+                packed_tokenId.shape, dtype=torch.float32, device=packed_tokenId.device
+            )
+        if packed_X_grad is None:
+            raise RuntimeError("pack_tokens_fn backward needs a gradient for packed_X")
+        X_grad, topk_weights_grad = ext.pack_kernel_backward(
+            packed_X_grad.contiguous(),
+            packed_topk_weights_grad.contiguous(),
+            packed_tokenId,
+            packed_expert,
+            topk_experts,
+        )
+        return X_grad, topk_weights_grad, None, None
+
+
+class CombineTokensFN(torch.autograd.Function):
+    """Reference: src/model/moe_ops.py:76-104."""
+
+    @staticmethod
+    def forward(ctx, packed_expert_outputs, packed_tokenId, packed_topk_weights, num_tokens,
+                hidden_dim) -> torch.Tensor:
+        ext = get_hip_extension()
+        pool = ext.combine_tokens_kernel(
+            packed_expert_outputs, packed_tokenId, packed_topk_weights, num_tokens, hidden_dim
+        )
+        ctx.save_for_backward(packed_expert_outputs, packed_tokenId, packed_topk_weights)
+        ctx.hidden_dim = hidden_dim
+        return pool
+
+    @staticmethod
+    def backward(ctx, d_resid_stream) -> tuple:
+        ext = get_hip_extension()
+        packed_expert_outputs, packed_tokenId, packed_topk_weights = ctx.saved_tensors
+        expert_output_grad, packed_topk_weights_grad = ext.combine_kernel_backward(
+            packed_expert_outputs,
+            packed_tokenId,
+            packed_topk_weights,
+            d_resid_stream.to(torch.float32).contiguous(),
+            ctx.hidden_dim,
+        )
+        return expert_output_grad, None, packed_topk_weights_grad, None, None
+
+
+class GroupedGEMM_FN(torch.autograd.Function):
+    """Reference: src/model/moe_ops.py:107-125."""
+
+    @staticmethod
+    def forward(ctx, X, expert_offset, weight) -> torch.Tensor:
+        ext = get_hip_extension()
+        ctx.save_for_backward(X, expert_offset, weight)
+        return ext.grouped_gemm_kernel(X, expert_offset, weight)
+
+    @staticmethod
+    def backward(ctx, out_grad) -> tuple:
+        ext = get_hip_extension()
+        X, expert_offset, weight = ctx.saved_tensors
+        out_grad = out_grad.contiguous()
+        dX = dW = None
+        if ctx.needs_input_grad[0]:
+            dX = ext.bwd_grouped_gemm_dX_kernel(weight, expert_offset, out_grad)
+        if ctx.needs_input_grad[2]:
+            dW = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, out_grad)
+        return dX, None, dW
+
+
+# --------------------------------------------------------------- layer ops
+
+
+class DispatchFN(torch.autograd.Function):
+    """Fused count + offsets + pack for the layer.
+
+    Forward returns (packed_X, packed_topk_weights, counts, offsets, token_id,
+    inv); the integer outputs are non-differentiable. Backward is the pack
+    backward driven by the inverse map.
+    """
+
+    @staticmethod
+    def forward(ctx, X, topk_weights, topk_experts, num_experts):
+        ext = get_hip_extension()
+        counts, offsets, packed_X, token_id, _expert, packed_w, inv = ext.dispatch_tokens(
+            X, topk_weights, topk_experts, num_experts
+        )
+        ctx.save_for_backward(inv)
+        ctx.mark_non_differentiable(counts, offsets, token_id, inv)
+        return packed_X, packed_w, counts, offsets, token_id, inv
+
+    @staticmethod
+    def backward(ctx, packed_X_grad, packed_w_grad, *_):
+        ext = get_hip_extension()
+        (inv,) = ctx.saved_tensors
+        if packed_w_grad is None:
+            packed_w_grad = torch.zeros(inv.numel(), dtype=torch.float32, device=inv.device)
+        X_grad, w_grad = ext.pack_backward_inv(
+            packed_X_grad.contiguous(), packed_w_grad.contiguous(), inv
+        )
+        return X_grad, w_grad, None, None
+
+
+class CombineInvFN(torch.autograd.Function):
+    """Combine by inverse map; output in ``out_dtype`` (float32 on the reference surface).
+
+    Backward accepts the grad in float32 or the activation dtype without a cast
+    pass and returns (expert_output_grad, None, packed_topk_weights_grad, None).
+    """
+
+    @staticmethod
+    def forward(ctx, packed_expert_outputs, inv, packed_topk_weights, out_dtype):
+        ext = get_hip_extension()
+        out = ext.combine_inv(packed_expert_outputs, inv, packed_topk_weights, out_dtype)
+        ctx.save_for_backward(packed_expert_outputs, inv, packed_topk_weights)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        ext = get_hip_extension()
+        y, inv, w = ctx.saved_tensors
+        if grad.dtype not in (torch.float32, y.dtype):
+            grad = grad.to(torch.float32)
+        dy, dw = ext.combine_backward_inv(y, inv, w, grad.contiguous())
+        return dy, None, dw, None
+
+
+def dispatch_fn(X, topk_weights, topk_experts, num_experts):
+    return DispatchFN.apply(X, topk_weights, topk_experts, num_experts)
+
+
+def combine_inv_fn(packed_expert_outputs, inv, packed_topk_weights, out_dtype=torch.float32):
+    return CombineInvFN.apply(packed_expert_outputs, inv, packed_topk_weights, out_dtype)

@@ -1,0 +1,75 @@
+"""The C ABI boundary on the CPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments before touching the GPU."""
+
+import re
+
+import pytest
+
+from nanotitan_amd import capi
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "nanotitan_moe.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nt_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    syms = declared_symbols()
+    for name in ("nt_count_experts", "nt_pack_tokens", "nt_combine_tokens", "nt_combine_backward",
+                 "nt_pack_backward", "nt_grouped_gemm", "nt_grouped_gemm_dx",
+                 "nt_grouped_gemm_dw", "nt_dispatch", "nt_strerror"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.load()
+    syms = declared_symbols()
+    assert set(syms) == set(capi.EXPORTS), "capi.EXPORTS out of sync with the header"
+    for name in syms:
+        assert hasattr(lib, name), name
+
+
+def test_strerror_and_version():
+    lib = capi.load()
+    assert lib.nt_strerror(capi.NT_OK) == b"success"
+    assert b"workspace" in lib.nt_strerror(capi.NT_ERR_WORKSPACE)
+    assert lib.nt_strerror(12345) == b"unknown status code"
+    assert lib.nt_version() >= 100
+
+
+def test_workspace_sizes_are_sane():
+    lib = capi.load()
+    assert lib.nt_dispatch_workspace_bytes(30720, 2, 8, 512, capi.NT_BF16) > 0
+    assert lib.nt_dispatch_workspace_bytes(-1, 2, 8, 512, capi.NT_BF16) == 0
+    assert lib.nt_combine_workspace_bytes(61440, 30720) >= 4 * (61440 + 2 * 30720)
+
+
+@pytest.mark.parametrize(
+    "fn,args,code",
+    [
+        ("nt_grouped_gemm", (99, None, None, None, 8, 16, 8, 8, None, None, 0, None),
+         capi.NT_ERR_DTYPE),
+        ("nt_grouped_gemm", (capi.NT_BF16, None, None, None, 0, 16, 8, 8, None, None, 0, None),
+         capi.NT_ERR_INVALID_ARG),
+        ("nt_grouped_gemm_dw", (capi.NT_BF16, None, None, None, 2000, 16, 8, 8, None, None, 0,
+                                None), capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_count_experts", (None, None, 10, 2, 4, None, None, 0, None), capi.NT_ERR_INVALID_ARG),
+        ("nt_count_experts", (None, None, 10, 2, 1025, None, None, 0, None),
+         capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_pack_tokens", (7, None, None, None, 4, 2, 8, 3, None, None, None, None, None, None,
+                            None, 0, None), capi.NT_ERR_DTYPE),
+        ("nt_combine_tokens", (capi.NT_F32, None, None, None, 4, 2, 8, None, None, 0, None),
+         capi.NT_ERR_INVALID_ARG),
+        ("nt_combine_inv", (capi.NT_F32, None, None, None, 4, 0, 8, capi.NT_F32, None, None),
+         capi.NT_ERR_INVALID_ARG),
+        ("nt_pack_backward_inv", (capi.NT_BF16, None, None, None, -3, 2, 8, None, None, None),
+         capi.NT_ERR_INVALID_ARG),
+    ],
+)
+def test_argument_errors_return_codes(fn, args, code):
+    lib = capi.load()
+    assert getattr(lib, fn)(*args) == code

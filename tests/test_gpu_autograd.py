@@ -1,0 +1,186 @@
+"""GPU: the autograd surface, mirroring the reference's own autograd tests
+(tests/test_pack_bwd.py, test_combine_bwd.py, test_moe_ops_bwd.py) with the
+same shapes, seeds and tolerances, and the MoE layer vs the CPU oracle."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCES = {
+    torch.float32: {"rtol": 1e-5, "atol": 1e-6},
+    torch.float16: {"rtol": 1e-2, "atol": 1e-2},
+    torch.bfloat16: {"rtol": 2e-2, "atol": 2e-2},
+}
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("num_tokens,top_k,d_model", [(3, 2, 8), (5, 3, 7)])
+def test_pack_backward_matches_reference(ext, dtype, num_tokens, top_k, d_model):
+    """reference tests/test_pack_bwd.py:20-55."""
+    from nanotitan_amd.moe_ops import pack_tokens_fn
+
+    torch.manual_seed(0)
+    device = "cuda"
+    x_ref = torch.randn(num_tokens, d_model, dtype=dtype, device=device, requires_grad=True)
+    x_hip = x_ref.detach().clone().requires_grad_(True)
+    w_ref = torch.rand(num_tokens, top_k, device=device, requires_grad=True)
+    w_hip = w_ref.detach().clone().requires_grad_(True)
+    topk = (torch.arange(num_tokens * top_k, device=device) % 3).reshape(num_tokens, top_k).to(
+        torch.int32)
+    counts = torch.bincount(topk.reshape(-1).long(), minlength=3)
+    offsets = torch.cat([counts.new_zeros(1), counts.cumsum(0)]).to(torch.int32)
+    packed, tid, expert, pw = pack_tokens_fn(x_hip, w_hip, topk, offsets.clone())
+    token_id = tid.long()
+    slot = (topk[token_id] == expert[:, None]).long().argmax(dim=1)
+    packed_ref = x_ref[token_id]
+    pw_ref = w_ref[token_id, slot]
+    torch.testing.assert_close(packed, packed_ref, **TOLERANCES[dtype])
+    torch.testing.assert_close(pw, pw_ref)
+    gp = torch.randn_like(packed_ref)
+    gw = torch.randn_like(pw_ref)
+    (packed_ref * gp).sum().add((pw_ref * gw).sum()).backward()
+    (packed * gp).sum().add((pw * gw).sum()).backward()
+    torch.testing.assert_close(x_hip.grad, x_ref.grad, **TOLERANCES[dtype])
+    torch.testing.assert_close(w_hip.grad, w_ref.grad, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("num_tokens,assignments,d_model", [(3, 6, 8), (5, 11, 7)])
+def test_combine_backward_matches_reference(ext, dtype, num_tokens, assignments, d_model):
+    """reference tests/test_combine_bwd.py:20-74 (uneven fan-in 3,2,2,2,2)."""
+    from nanotitan_amd.moe_ops import combine_tokens_fn
+
+    torch.manual_seed(0)
+    device = "cuda"
+    y_ref = torch.randn(assignments, d_model, dtype=dtype, device=device, requires_grad=True)
+    g_ref = torch.randn(assignments, device=device, requires_grad=True)
+    tid = torch.tensor([i % num_tokens for i in range(assignments)], device=device,
+                       dtype=torch.int32)
+    y_hip = y_ref.detach().clone().requires_grad_(True)
+    g_hip = g_ref.detach().clone().requires_grad_(True)
+    out_ref = torch.zeros(num_tokens, d_model, device=device, dtype=torch.float32)
+    out_ref.index_add_(0, tid.long(), y_ref.float() * g_ref[:, None])
+    out_hip = combine_tokens_fn(y_hip, tid, g_hip, num_tokens, d_model)
+    torch.testing.assert_close(out_hip, out_ref, **TOLERANCES[dtype])
+    grad = torch.randn_like(out_ref)
+    out_ref.backward(grad)
+    out_hip.backward(grad)
+    torch.testing.assert_close(y_hip.grad, y_ref.grad, **TOLERANCES[dtype])
+    torch.testing.assert_close(g_hip.grad, g_ref.grad, **TOLERANCES[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("num_tokens,top_k,d_model", [(3, 2, 8), (5, 3, 7)])
+def test_pack_then_combine_backward(ext, dtype, num_tokens, top_k, d_model):
+    """reference tests/test_moe_ops_bwd.py:21-55."""
+    from nanotitan_amd.moe_ops import combine_tokens_fn, pack_tokens_fn
+
+    torch.manual_seed(0)
+    device = "cuda"
+    x_ref = torch.randn(num_tokens, d_model, dtype=dtype, device=device, requires_grad=True)
+    x_hip = x_ref.detach().clone().requires_grad_(True)
+    w_ref = torch.rand(num_tokens, top_k, device=device, requires_grad=True)
+    w_hip = w_ref.detach().clone().requires_grad_(True)
+    topk = (torch.arange(num_tokens * top_k, device=device) % 3).reshape(num_tokens, top_k).to(
+        torch.int32)
+    counts = torch.bincount(topk.reshape(-1).long(), minlength=3)
+    offsets = torch.cat([counts.new_zeros(1), counts.cumsum(0)]).to(torch.int32)
+    px, tid, _, pw = pack_tokens_fn(x_hip, w_hip, topk, offsets.clone())
+    y_hip = combine_tokens_fn(px, tid, pw, num_tokens, d_model)
+    y_ref = torch.zeros(num_tokens, d_model, dtype=torch.float32, device=device)
+    for k in range(top_k):
+        y_ref = y_ref + x_ref.float() * w_ref[:, k, None]
+    torch.testing.assert_close(y_hip, y_ref, **TOLERANCES[dtype])
+    grad = torch.randn_like(y_ref)
+    y_ref.backward(grad)
+    y_hip.backward(grad)
+    torch.testing.assert_close(x_hip.grad, x_ref.grad, **TOLERANCES[dtype])
+    torch.testing.assert_close(w_hip.grad, w_ref.grad, **TOLERANCES[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_expert_ffn_swiglu_vs_oracle(ext, dtype):
+    """reference tests/test_grouped_gemm.py:211-257 (offsets [0,3,4,8], d=8, ffn=16)."""
+    from nanotitan_amd.layer import ExpertFFN, ModelShardSpec
+
+    torch.manual_seed(0)
+    cfg = SimpleNamespace(num_experts=3, d_model=8, ffn_in=16, dtype=dtype, moe_backend="hip")
+    spec = ModelShardSpec(per_rank_expert=3, end_expert_id=3)
+    ffn = ExpertFFN(cfg, spec).cuda()
+    offsets = torch.tensor([0, 3, 4, 8], dtype=torch.int32, device="cuda")
+    X = torch.randn(8, 8, dtype=dtype, device="cuda", requires_grad=True)
+    out = ffn(X, offsets)
+    d_out = torch.randn_like(out)
+    out.backward(d_out)
+    # CPU float64 reference of the same SwiGLU experts
+    Xr = X.detach().cpu().double().requires_grad_(True)
+    Ws = {n: getattr(ffn, n).detach().cpu().double().requires_grad_(True)
+          for n in ("W_gate", "W_val", "W_out")}
+    rows = []
+    for e in range(3):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        xe = Xr[a:b]
+        h = torch.nn.functional.silu(xe @ Ws["W_gate"][e]) * (xe @ Ws["W_val"][e])
+        rows.append(h @ Ws["W_out"][e])
+    ref = torch.cat(rows)
+    ref.backward(d_out.cpu().double())
+    tol = dict(rtol=1e-4, atol=5e-4) if dtype == torch.float32 else dict(rtol=3e-2, atol=3e-2)
+    torch.testing.assert_close(out.detach().cpu().double(), ref.detach(), **tol)
+    torch.testing.assert_close(X.grad.cpu().double(), Xr.grad, **tol)
+    for n in ("W_gate", "W_val", "W_out"):
+        torch.testing.assert_close(getattr(ffn, n).grad.cpu().double(), Ws[n].grad, **tol)
+
+
+@pytest.mark.parametrize("cfg_id,T,ffn", [(1, 1024, "gelu"), (2, 2048, "gelu"), (3, 1024, "gelu"),
+                                          (2, 512, "swiglu")])
+def test_moe_layer_fwd_bwd_vs_oracle(ext, cfg_id, T, ffn):
+    """Whole hot path from router logits, forward + backward, vs the oracle torch path."""
+    from nanotitan_amd.layer import moe_forward_from_logits
+    from nanotitan_amd.moe_ops import grouped_gemm_fn
+
+    d = O.make_inputs(cfg_id, T=T, ffn=ffn)
+    c = d["cfg"]
+    Wg = {n: w.cuda().requires_grad_(True) for n, w in d["weights"].items()}
+
+    class FFN(torch.nn.Module):
+        def forward(self, px, off):
+            if ffn == "gelu":
+                h = torch.nn.functional.gelu(grouped_gemm_fn(px, Wg["up"], off))
+                return grouped_gemm_fn(h, Wg["down"], off)
+            h = torch.nn.functional.silu(grouped_gemm_fn(px, Wg["gate"], off)) * grouped_gemm_fn(
+                px, Wg["val"], off)
+            return grouped_gemm_fn(h, Wg["out"], off)
+
+    x = d["X"].cuda().requires_grad_(True)
+    logits = d["logits"].cuda().requires_grad_(True)
+    out, counts, _ = moe_forward_from_logits(x, logits, FFN(), c.E, c.k)
+    out.backward(d["dY"].cuda())
+    ref_out, ref = O.moe_layer_torch(d["X"], d["logits"], d["weights"], c.k, ffn=ffn, dY=d["dY"])
+    tol = dict(rtol=1e-4, atol=1e-4) if c.dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.detach().cpu().float(), ref_out.float(), **tol)
+    torch.testing.assert_close(x.grad.cpu().float(), ref["x"].float(), **tol)
+    for n, w in Wg.items():
+        torch.testing.assert_close(w.grad.cpu().float(), ref[n].float(), **tol)
+    torch.testing.assert_close(logits.grad.cpu().float(), ref["logits"].float(),
+                               rtol=tol["rtol"], atol=tol["atol"] / 10)
+
+
+def test_moe_module_four_arg_backend(ext):
+    """MoE(cfg, spec) builds the HIP backend with the 4-argument constructor and returns stats."""
+    from nanotitan_amd.layer import MoE
+
+    cfg = SimpleNamespace(d_model=64, num_experts=16, top_k=4, ffn_in=128, dtype=torch.bfloat16,
+                          moe_router_dtype=torch.float32, moe_backend="hip", router_alpha=0.01)
+    moe = MoE(cfg).cuda()
+    x = torch.randn(4, 16, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    y, stats = moe(x)
+    assert y.shape == x.shape and y.dtype == x.dtype
+    (y.float().square().mean() + stats.aux_loss).backward()
+    assert int(stats.tokens_per_expert.sum()) == 4 * 16 * 4
+    assert x.grad is not None and moe.router.weight.grad is not None

@@ -1,0 +1,158 @@
+"""GPU parity: combine forward/backward and pack backward vs the CPU oracle.
+
+Combine forward is bit-exact against the oracle's ordered fp32 sum; dy and
+pack-backward dX (fp32 ordered sum, one cast) are bit-exact; the gate
+gradient dw is a dot product compared within rel 1e-5 (fp32 accumulation,
+fixed reduction order on the GPU).
+"""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests.conftest import GOLDEN
+from tests.test_gpu_dispatch import bits
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16, torch.float64]
+DW_TOL = dict(rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("case", ["top1", "top2"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_combine_reference_kat(ext, case, dtype):
+    """reference tests/test_combine.py:12-90."""
+    kat = json.loads((GOLDEN / "combine_kat.json").read_text())[case]
+    y = torch.tensor(kat["expert_outputs"], dtype=dtype, device="cuda")
+    tid = torch.tensor(kat["packed_tokenId"], dtype=torch.int32, device="cuda")
+    w = torch.tensor(kat["packed_topk_weights"], dtype=torch.float32, device="cuda")
+    out = ext.combine_tokens_kernel(y, tid, w, kat["num_tokens"], 2)
+    assert out.dtype == torch.float32
+    want = O.combine_tokens(y.cpu(), tid.cpu(), w.cpu(), kat["num_tokens"])
+    assert torch.equal(bits(out), bits(torch.from_numpy(want)))
+    tol = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 2e-2}[dtype]
+    torch.testing.assert_close(out.cpu().to(dtype).float(),
+                               torch.tensor(kat["expected"]).to(dtype).float(), rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,A,d", [(3, 6, 8), (5, 11, 7), (100, 1000, 64), (64, 64 * 300, 24),
+                                   (1, 1, 1), (50, 0, 16)])
+def test_combine_generic_bit_exact(ext, dtype, T, A, d):
+    """Arbitrary token-id multiplicity (reference tests/test_combine_bwd.py:39-43 style)."""
+    g = torch.Generator().manual_seed(T + A + d)
+    y = torch.randn(A, d, generator=g).to(dtype)
+    w = torch.randn(A, generator=g)
+    tid = torch.randint(0, T, (A,), generator=g, dtype=torch.int32)
+    out = ext.combine_tokens_kernel(y.cuda(), tid.cuda(), w.cuda(), T, d)
+    want = O.combine_tokens(y, tid, w, T)
+    assert torch.equal(bits(out), bits(torch.from_numpy(want)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,A,d", [(3, 6, 8), (5, 11, 7), (200, 1600, 40), (4, 0, 8)])
+def test_combine_backward_generic(ext, dtype, T, A, d):
+    g = torch.Generator().manual_seed(A + 5)
+    y = torch.randn(A, d, generator=g).to(dtype)
+    w = torch.randn(A, generator=g)
+    tid = torch.tensor([i % T for i in range(A)], dtype=torch.int32)
+    dY = torch.randn(T, d, generator=g)
+    dy, dw = ext.combine_kernel_backward(y.cuda(), tid.cuda(), w.cuda(), dY.cuda(), d)
+    want_dy, want_dw = O.combine_backward(y, tid, w, dY, out_dtype=dtype)
+    assert torch.equal(bits(dy), bits(want_dy))
+    np.testing.assert_allclose(dw.cpu().numpy(), want_dw, **DW_TOL)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,k,E,d", [(3, 2, 3, 8), (5, 3, 3, 7), (500, 8, 64, 96), (77, 1, 4, 5)])
+def test_pack_backward_generic_and_inv(ext, dtype, T, k, E, d):
+    g = torch.Generator().manual_seed(T * k)
+    X = torch.randn(T, d, generator=g).to(dtype)
+    w = torch.rand(T, k, generator=g)
+    # distinct experts per token, like torch.topk
+    topk = torch.argsort(torch.rand(T, E, generator=g), dim=1)[:, :k].to(torch.int32)
+    counts, offsets, p = O.dispatch(X, w, topk, E)
+    A = T * k
+    dpX = torch.randn(A, d, generator=g).to(dtype)
+    dpw = torch.randn(A, generator=g)
+    want_dX, want_dw = O.pack_backward(dpX, dpw, p.token_id, p.expert, topk, out_dtype=dtype)
+    dX, dw = ext.pack_kernel_backward(dpX.cuda(), dpw.cuda(), torch.from_numpy(p.token_id).cuda(),
+                                      torch.from_numpy(p.expert).cuda(), topk.cuda())
+    assert torch.equal(bits(dX), bits(want_dX))
+    assert torch.equal(bits(dw), bits(torch.from_numpy(want_dw)))
+    dX2, dw2 = ext.pack_backward_inv(dpX.cuda(), dpw.cuda(), torch.from_numpy(p.inv).cuda())
+    assert torch.equal(bits(dX2), bits(want_dX))
+    assert torch.equal(bits(dw2), bits(torch.from_numpy(want_dw)))
+
+
+def test_pack_backward_first_match_rule(ext):
+    """Duplicate experts in a row: the reference's first-match rule (backward_pack_kernel.cu:35-42)."""
+    topk = torch.tensor([[2, 2], [0, 1]], dtype=torch.int32)
+    tid = torch.tensor([0, 0, 1, 1], dtype=torch.int32)
+    ex = torch.tensor([2, 2, 0, 1], dtype=torch.int32)
+    dpw = torch.tensor([1.0, 2.0, 3.0, 4.0])
+    dX, dw = ext.pack_kernel_backward(torch.zeros(4, 3, device="cuda"), dpw.cuda(), tid.cuda(),
+                                      ex.cuda(), topk.cuda())
+    assert dw.tolist() == [[3.0, 0.0], [3.0, 4.0]]
+
+
+@pytest.mark.parametrize("cfg_id,T", [(2, 30720), (3, 8192), (5, 4096)])
+def test_combine_inv_matches_generic_and_oracle(ext, cfg_id, T):
+    """Layer path (inverse map) == reference surface (token ids) == oracle, bit for bit."""
+    d = O.make_inputs(cfg_id, T=T, with_weights=False)
+    c = d["cfg"]
+    gates, idx, _ = O.route(d["logits"], c.k)
+    dd = 128 if cfg_id == 5 else c.d
+    X = d["X"][:, :dd].contiguous()
+    counts, offsets, p = O.dispatch(X, gates, idx, c.E)
+    g = torch.Generator().manual_seed(cfg_id)
+    y = torch.randn(T * c.k, dd, generator=g).to(c.dtype)
+    tid = torch.from_numpy(p.token_id)
+    pw = torch.from_numpy(p.packed_w)
+    inv = torch.from_numpy(p.inv)
+    want = O.combine_tokens(y, tid, pw, T)
+    a = ext.combine_tokens_kernel(y.cuda(), tid.cuda(), pw.cuda(), T, dd)
+    b = ext.combine_inv(y.cuda(), inv.cuda(), pw.cuda(), torch.float32)
+    c16 = ext.combine_inv(y.cuda(), inv.cuda(), pw.cuda(), c.dtype)
+    assert torch.equal(bits(a), bits(torch.from_numpy(want)))
+    assert torch.equal(bits(b), bits(a))
+    assert torch.equal(bits(c16), bits(a.to(c.dtype)))
+    # backward: inverse-map form == generic form, bit for bit; dw within tolerance of oracle
+    dY = d["dY"][:, :dd].float()
+    dy1, dw1 = ext.combine_kernel_backward(y.cuda(), tid.cuda(), pw.cuda(), dY.cuda(), dd)
+    dy2, dw2 = ext.combine_backward_inv(y.cuda(), inv.cuda(), pw.cuda(), dY.cuda())
+    dy3, dw3 = ext.combine_backward_inv(y.cuda(), inv.cuda(), pw.cuda(), dY.to(c.dtype).cuda())
+    assert torch.equal(bits(dy1), bits(dy2)) and torch.equal(bits(dw1), bits(dw2))
+    want_dy, want_dw = O.combine_backward(y, tid, pw, dY, out_dtype=c.dtype)
+    assert torch.equal(bits(dy1), bits(want_dy))
+    np.testing.assert_allclose(dw1.cpu().numpy(), want_dw, **DW_TOL)
+    want_dy3, want_dw3 = O.combine_backward(y, tid, pw, dY.to(c.dtype).float(), out_dtype=c.dtype)
+    assert torch.equal(bits(dy3), bits(want_dy3))
+    np.testing.assert_allclose(dw3.cpu().numpy(), want_dw3, **DW_TOL)
+
+
+def test_combine_is_deterministic(ext):
+    g = torch.Generator().manual_seed(9)
+    y = torch.randn(8192, 256, generator=g).to(torch.bfloat16).cuda()
+    tid = torch.randint(0, 1000, (8192,), generator=g, dtype=torch.int32).cuda()
+    w = torch.rand(8192, generator=g).cuda()
+    a = ext.combine_tokens_kernel(y, tid, w, 1000, 256)
+    b = ext.combine_tokens_kernel(y, tid, w, 1000, 256)
+    assert torch.equal(bits(a), bits(b))
+    dY = torch.randn(1000, 256, generator=g).cuda()
+    r1 = ext.combine_kernel_backward(y, tid, w, dY, 256)
+    r2 = ext.combine_kernel_backward(y, tid, w, dY, 256)
+    assert torch.equal(bits(r1[1]), bits(r2[1]))
+
+
+def test_combine_rejects_non_fp32_grad(ext):
+    y = torch.randn(4, 2, device="cuda")
+    tid = torch.zeros(4, dtype=torch.int32, device="cuda")
+    w = torch.ones(4, device="cuda")
+    with pytest.raises(RuntimeError, match="float32"):
+        ext.combine_kernel_backward(y, tid, w, torch.zeros(1, 2, device="cuda",
+                                                           dtype=torch.float16), 2)

@@ -1,0 +1,141 @@
+"""GPU parity: expert-grouped GEMM forward, dX and dW vs the float64 oracle.
+
+Tolerances are the reference's (tests/test_grouped_gemm.py:35-39): fp32
+rtol 1e-4 / atol 5e-4, bf16 and fp16 2e-2 (scaled by the reduction length
+where the values grow with it).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+TOL = {
+    torch.float32: dict(rtol=1e-4, atol=5e-4),
+    torch.float64: dict(rtol=1e-9, atol=1e-9),
+    torch.float16: dict(rtol=2e-2, atol=2e-2),
+    torch.bfloat16: dict(rtol=2e-2, atol=2e-2),
+}
+
+
+def check(got, want, dtype, scale=1.0):
+    """Compare against the fp64 oracle rounded to dtype (the best a dtype output can do)."""
+    want_c = want.to(dtype).double()
+    tol = dict(TOL[dtype])
+    tol["atol"] = tol["atol"] * scale
+    torch.testing.assert_close(got.cpu().double(), want_c, **tol)
+
+
+def run_all(ext, X, W, offsets, G):
+    Xg, Wg, og, Gg = X.cuda(), W.cuda(), offsets.cuda(), G.cuda()
+    out = ext.grouped_gemm_kernel(Xg, og, Wg)
+    dX = ext.bwd_grouped_gemm_dX_kernel(Wg, og, Gg)
+    dW = ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg)
+    torch.cuda.synchronize()
+    return out, dX, dW
+
+
+@pytest.mark.parametrize("dtype", DTYPES + [torch.float64])
+@pytest.mark.parametrize("shape", [(4, 2, 4, 4), (128, 4, 16, 32), (8192, 3, 1, 8192)])
+def test_small_smoke_shapes(ext, dtype, shape):
+    """reference tests/test_grouped_gemm.py:51-82 shapes (even splits i*A//E)."""
+    A, E, K, N = shape
+    g = torch.Generator().manual_seed(A + K)
+    X = torch.randn(A, K, generator=g).to(dtype)
+    W = torch.randn(E, K, N, generator=g).to(dtype)
+    offsets = torch.tensor([i * A // E for i in range(E + 1)], dtype=torch.int32)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    out, dX, dW = run_all(ext, X, W, offsets, G)
+    check(out, O.grouped_gemm(X, offsets, W), dtype, scale=max(1, K) ** 0.5)
+    check(dX, O.grouped_gemm_dx(W, offsets, G), dtype, scale=max(1, N) ** 0.5)
+    check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(1, A // E) ** 0.5)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("K,N", [(2048, 8192), (8192, 2048)])
+def test_moe_projection_counts_3_1_4(ext, dtype, K, N):
+    """reference tests/test_grouped_gemm.py:85-145: counts [3,1,4], offsets [0,3,4,8]."""
+    g = torch.Generator().manual_seed(K)
+    offsets = torch.tensor([0, 3, 4, 8], dtype=torch.int32)
+    X = torch.randn(8, K, generator=g).to(dtype)
+    W = (torch.randn(3, K, N, generator=g) / K ** 0.5).to(dtype)
+    G = torch.randn(8, N, generator=g).to(dtype)
+    out, dX, dW = run_all(ext, X, W, offsets, G)
+    check(out, O.grouped_gemm(X, offsets, W), dtype)
+    check(dX, O.grouped_gemm_dx(W, offsets, G), dtype, scale=(N / K) ** 0.5)
+    check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=2.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("counts", [[0, 5, 0, 130, 1, 0], [257, 0, 0, 0], [0, 0, 0],
+                                    [1, 1, 1, 1, 1, 1, 1, 1], [700, 3, 129, 128, 127]])
+def test_empty_and_skewed_experts(ext, dtype, counts):
+    """Empty experts, M_e = 1, tile-edge rows; dW of an empty expert is exactly zero."""
+    K, N = 96, 136
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    A = int(offsets[-1]) + 5  # rows past offsets[E] are never read or written
+    g = torch.Generator().manual_seed(sum(counts) + len(counts))
+    X = torch.randn(A, K, generator=g).to(dtype)
+    W = (torch.randn(len(counts), K, N, generator=g) / K ** 0.5).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    out, dX, dW = run_all(ext, X, W, offsets, G)
+    used = int(offsets[-1])
+    check(out[:used], O.grouped_gemm(X, offsets, W)[:used], dtype)
+    check(dX[:used], O.grouped_gemm_dx(W, offsets, G)[:used], dtype, scale=2.0)
+    check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(counts + [1]) ** 0.5)
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert not dW[e].any()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("K,N", [(2048, 8192), (8192, 2048)])
+def test_autograd_wrapper_noncontiguous_grad(ext, dtype, K, N):
+    """reference tests/test_grouped_gemm.py:148-208, including the transposed d_out."""
+    from nanotitan_amd.moe_ops import grouped_gemm_fn
+
+    torch.manual_seed(0)
+    offsets = torch.tensor([0, 3, 4, 8], dtype=torch.int32, device="cuda")
+    X = torch.randn(8, K, dtype=dtype, device="cuda", requires_grad=True)
+    W = (torch.randn(3, K, N, dtype=dtype, device="cuda") / K ** 0.5).requires_grad_(True)
+    out = grouped_gemm_fn(X, W, offsets)
+    d_out = torch.randn(N, 8, dtype=dtype, device="cuda").T
+    out.backward(d_out)
+    Xc, Wc, Gc = X.detach().cpu(), W.detach().cpu(), d_out.detach().cpu()
+    off = offsets.cpu()
+    check(out.detach(), O.grouped_gemm(Xc, off, Wc), dtype)
+    check(X.grad, O.grouped_gemm_dx(Wc, off, Gc), dtype, scale=(N / K) ** 0.5)
+    check(W.grad, O.grouped_gemm_dw(Xc, off, Gc), dtype, scale=2.0)
+
+
+@pytest.mark.parametrize("cfg_id,T", [(2, 4096), (3, 4096)])
+def test_config_shapes_routed(ext, cfg_id, T):
+    """Real routed segment sizes at the configs' widths (C3: Zipf skew, tiny experts)."""
+    d = O.make_inputs(cfg_id, T=T)
+    c = d["cfg"]
+    gates, idx, _ = O.route(d["logits"], c.k)
+    counts = O.count_experts(idx, None, c.E)
+    offsets = torch.from_numpy(O.offsets_from_counts(counts))
+    A = T * c.k
+    g = torch.Generator().manual_seed(cfg_id)
+    X = torch.randn(A, c.d, generator=g).to(c.dtype)
+    W = d["weights"]["up"]
+    G = torch.randn(A, c.f, generator=g).to(c.dtype)
+    out, dX, dW = run_all(ext, X, W, offsets, G)
+    check(out, O.grouped_gemm(X, offsets, W), c.dtype)
+    check(dX, O.grouped_gemm_dx(W, offsets, G), c.dtype)
+    check(dW, O.grouped_gemm_dw(X, offsets, G), c.dtype, scale=max(int(counts.max()), 1) ** 0.5)
+
+
+def test_gemm_is_deterministic(ext):
+    g = torch.Generator().manual_seed(3)
+    offsets = torch.tensor([0, 1000, 1000, 3000], dtype=torch.int32).cuda()
+    X = torch.randn(3000, 256, generator=g).to(torch.bfloat16).cuda()
+    G = torch.randn(3000, 512, generator=g).to(torch.bfloat16).cuda()
+    a = ext.bwd_grouped_gemm_dW_kernel(X, offsets, G)
+    b = ext.bwd_grouped_gemm_dW_kernel(X, offsets, G)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
