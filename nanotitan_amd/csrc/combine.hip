@@ -228,8 +228,13 @@ combine_kernel(const typename elem<T>::storage* __restrict__ y, ListSrc src,
       const float wp = w[p];
       float x[VE];
       load_vec<T, VE>(y + (int64_t)p * d + h, x);
+      // The product is rounded to fp32 before the add (no fused multiply-add),
+      // exactly as a sequential index_add_ of a pre-multiplied tensor.
+      {
+#pragma clang fp contract(off)
 #pragma unroll
-      for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], __fmul_rn(wp, x[v]));
+        for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp * x[v];
+      }
     }
     store_vec<TO, VE>(out + t * d + h, acc);
   }

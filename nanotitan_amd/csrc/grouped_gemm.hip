@@ -104,28 +104,47 @@ struct mfma_op<f16> {
   }
 };
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kLdsStride = kBK + 8;  // elements; 144 B rows keep 16-B reads conflict-free
 
-// K-contiguous operand: element (row, kk) at p[row*ld + kk].
-// One 16-byte chunk (8 elements along kk) per slot.
+// Operand tiles are fetched with raw buffer loads: one wave-uniform
+// descriptor per tile and k-step (base address + byte range), a 32-bit
+// per-lane offset, and the hardware's range check returning zeros for any
+// offset past the range. Lanes whose slot is outside the tile get kOob.
+// No branches or selects around the loads, and no 64-bit address registers.
+constexpr uint32_t kBufConfig = 0x00020000u;  // gfx9 buffer descriptor word 3
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = (int32_t)(bytes <= 0 ? 0 : (bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, (int)kBufConfig);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// K-contiguous operand: element (row, kk) at p[row*ld + kk]; `rows` valid
+// rows, `kleft` valid kk from this k-step on. One 16-byte chunk (8 elements
+// along kk) per slot.
 template <int ROWS>
 struct LoaderK {
   static constexpr int kChunks = ROWS * kBK / 8 / kGemmThreads;
+  static constexpr int kLoads = kChunks;   // buffer loads per tile
+  static constexpr int kStores = kChunks;  // LDS writes per tile
   uint4 r[kChunks];
-  __device__ void load(const uint16_t* __restrict__ p, int64_t ld, int64_t rows_valid,
-                       int64_t k_valid) {
+  __device__ void load(const uint16_t* p, int64_t ld, int64_t rows, int64_t kleft) {
+    const int64_t kv = kleft < kBK ? kleft : kBK;
+    const int64_t rv = rows < ROWS ? rows : ROWS;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p, ((rv - 1) * ld + kv) * 2);
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int q = threadIdx.x + i * kGemmThreads;
       const int row = q / (kBK / 8);
       const int kc = (q % (kBK / 8)) * 8;
-      if (row < rows_valid && kc < k_valid)
-        r[i] = *reinterpret_cast<const uint4*>(p + (int64_t)row * ld + kc);
-      else
-        r[i] = make_uint4(0, 0, 0, 0);
+      const uint32_t off = kc < kv ? (uint32_t)(row * ld + kc) * 2u : kOob;
+      r[i] = buf_load16(rs, off);
     }
   }
   __device__ void store(uint16_t* s) const {
@@ -139,28 +158,34 @@ struct LoaderK {
   }
 };
 
-// M-contiguous operand: element (row, kk) at p[kk*ld + row]. Each slot is a
-// 4 (kk) x 8 (row) block: four 16-byte loads, transposed in registers into
-// eight 8-byte LDS writes (row-major, kk contiguous).
+// M-contiguous operand: element (row, kk) at p[kk*ld + row]; `rows` valid
+// rows (columns in memory), `kleft` valid kk. Each slot is a 4 (kk) x 8 (row)
+// block: four 16-byte loads, transposed in registers into eight 8-byte LDS
+// writes (row-major, kk contiguous). Consecutive lanes take consecutive kk
+// blocks of the same rows, so each group of 16 lanes writes 128 contiguous
+// LDS bytes of one row (bank-conflict free); across the wave the four row
+// groups read 64 contiguous bytes of every HBM row they touch.
 template <int ROWS>
 struct LoaderM {
   static constexpr int kBlocks = ROWS * kBK / 32 / kGemmThreads;
   static_assert(kBlocks >= 1, "tile too small for one 4x8 block per thread");
+  static constexpr int kLoads = 4 * kBlocks;
+  static constexpr int kStores = 8 * kBlocks;
   uint4 r[kBlocks][4];
-  __device__ void load(const uint16_t* __restrict__ p, int64_t ld, int64_t rows_valid,
-                       int64_t k_valid) {
+  __device__ void load(const uint16_t* p, int64_t ld, int64_t rows, int64_t kleft) {
+    const int64_t kv = kleft < kBK ? kleft : kBK;
+    const int64_t cv = rows < ld ? rows : ld;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p, ((kv - 1) * ld + cv) * 2);
 #pragma unroll
     for (int i = 0; i < kBlocks; ++i) {
       const int q = threadIdx.x + i * kGemmThreads;
-      const int mb = (q % (ROWS / 8)) * 8;
-      const int kb = (q / (ROWS / 8)) * 4;
+      const int kb = (q % (kBK / 4)) * 4;
+      const int mb = (q / (kBK / 4)) * 8;
+      const bool ok = mb < cv;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int kk = kb + rr;
-        if (mb < rows_valid && kk < k_valid)
-          r[i][rr] = *reinterpret_cast<const uint4*>(p + (int64_t)kk * ld + mb);
-        else
-          r[i][rr] = make_uint4(0, 0, 0, 0);
+        const uint32_t off = ok ? (uint32_t)((kb + rr) * ld + mb) * 2u : kOob;
+        r[i][rr] = buf_load16(rs, off);
       }
     }
   }
@@ -168,8 +193,8 @@ struct LoaderM {
 #pragma unroll
     for (int i = 0; i < kBlocks; ++i) {
       const int q = threadIdx.x + i * kGemmThreads;
-      const int mb = (q % (ROWS / 8)) * 8;
-      const int kb = (q / (ROWS / 8)) * 4;
+      const int kb = (q % (kBK / 4)) * 4;
+      const int mb = (q / (kBK / 4)) * 8;
       const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&r[i][0]);
       const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&r[i][1]);
       const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&r[i][2]);
@@ -200,11 +225,6 @@ struct LoaderSel<false, ROWS> {
   typedef LoaderM<ROWS> type;
 };
 
-template <typename T>
-__device__ __forceinline__ uint16_t cvt_out(float v) {
-  return elem<T>::store(v);
-}
-
 struct GemmArgs {
   const void* a;  // fwd: X     dX: dOut   dW: X
   const void* b;  // fwd: W     dX: W      dW: dOut
@@ -212,22 +232,59 @@ struct GemmArgs {
   int32_t E;
   int64_t A, K, N;
   void* out;
-  int32_t ntn;  // output tiles along the n dimension
-  int32_t ntm;  // dW only: output tiles along K
+  int32_t ntn;      // output tiles along the n dimension
+  int32_t ntm;      // dW only: output tiles along K
+  int64_t mtiles;   // m-tile slots enumerated by the grid (upper bound for fwd / dX)
 };
 
-// One 128x128 output tile per workgroup.
-template <typename T, int MODE>
+// Workgroup ids are dealt to the 8 XCDs round-robin; renumber them so each
+// XCD receives a contiguous range of logical tiles (tiles that share operand
+// panels then share that XCD's L2).
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t G) {
+  constexpr int kXcd = 8;
+  const int64_t q = G / kXcd, r = G % kXcd;
+  const int64_t x = bid % kXcd, s = bid / kXcd;
+  return x * q + (x < r ? x : r) + s;
+}
+
+// Logical tile -> (m-tile, n-tile): groups of kGroupM m-tiles, m fastest
+// inside a group, so neighbouring logical tiles reuse both A and B panels.
+constexpr int kGroupM = 8;
+__device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int ntn, int64_t& mt,
+                                            int& nt) {
+  const int64_t per_group = (int64_t)kGroupM * ntn;
+  const int64_t grp = logical / per_group;
+  const int64_t rem = logical - grp * per_group;
+  const int64_t gm0 = grp * kGroupM;
+  const int64_t gsz = (mtiles - gm0) < kGroupM ? (mtiles - gm0) : kGroupM;
+  mt = gm0 + rem % gsz;
+  nt = (int)(rem / gsz);
+}
+
+// One BM x BN output tile per workgroup of 4 waves (2 x 2); each wave owns a
+// (BM/2) x (BN/2) block of 32x32 MFMA tiles. The MFMA is issued with the B
+// fragment as its first operand, so each lane's accumulator holds 4
+// consecutive output columns of one output row (packable 8-byte groups).
+// K advances 64 per iteration through two LDS stages (one barrier per
+// iteration); the epilogue stages the bf16/fp16 tile through LDS and writes
+// 16-byte row chunks.
+template <typename T, int MODE, int BM, int BN>
 __global__ void __launch_bounds__(kGemmThreads)
+__attribute__((amdgpu_waves_per_eu(1, BM * BN >= 256 * 128 ? 1 : 2)))
 gg_mfma_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[kBM * kLdsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t s_b[kBN * kLdsStride];
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int kStageA = BM * kLdsStride;
+  constexpr int kStage = (BM + BN) * kLdsStride;
+  constexpr int kEpiStride = BN + 8;
+  constexpr int kLdsElems = (2 * kStage > BM * kEpiStride) ? 2 * kStage : BM * kEpiStride;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[kLdsElems];
   __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
 
   constexpr bool kAK = MODE != kDw;   // A operand K-contiguous?
   constexpr bool kBK_ = MODE == kDx;  // B operand K-contiguous?
-  typedef typename LoaderSel<kAK, kBM>::type LA;
-  typedef typename LoaderSel<kBK_, kBN>::type LB;
+  typedef typename LoaderSel<kAK, BM>::type LA;
+  typedef typename LoaderSel<kBK_, BN>::type LB;
 
   const uint16_t* pa;
   const uint16_t* pb;
@@ -235,9 +292,10 @@ gg_mfma_kernel(GemmArgs g) {
   uint16_t* po;
   int64_t ldo;
 
-  const int64_t bid = blockIdx.x;
-  const int nt = (int)(bid % g.ntn);
-  const int64_t mt = bid / g.ntn;
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  int64_t mt;
+  int nt;
+  tile_coords(logical, g.mtiles, g.ntn, mt, nt);
 
   if (MODE == kDw) {
     const int e = (int)(mt / g.ntm);
@@ -245,38 +303,38 @@ gg_mfma_kernel(GemmArgs g) {
     int64_t r0, r1;
     expert_rows(g.offsets, e, g.A, r0, r1);
     kred = r1 - r0;
-    pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * kBM;
+    pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * BM;
     lda = g.K;
-    pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * kBN;
+    pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * BN;
     ldb = g.N;
-    rows_valid = g.K - (int64_t)mtl * kBM;
-    cols_valid = g.N - (int64_t)nt * kBN;
-    po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * kBM * g.N +
-         (int64_t)nt * kBN;
+    rows_valid = g.K - (int64_t)mtl * BM;
+    cols_valid = g.N - (int64_t)nt * BN;
+    po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * BM * g.N +
+         (int64_t)nt * BN;
     ldo = g.N;
   } else {
     int e;
     int64_t r0, r1, mtl;
-    if (!map_m_tile(g.offsets, g.E, g.A, kBM, mt, s_pref, e, r0, r1, mtl)) return;
-    const int64_t row0 = r0 + mtl * kBM;
+    if (!map_m_tile(g.offsets, g.E, g.A, BM, mt, s_pref, e, r0, r1, mtl)) return;
+    const int64_t row0 = r0 + mtl * BM;
     rows_valid = r1 - row0;
     if (MODE == kFwd) {
       pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
       lda = g.K;
-      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * kBN;
+      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN;
       ldb = g.N;
-      cols_valid = g.N - (int64_t)nt * kBN;
+      cols_valid = g.N - (int64_t)nt * BN;
       kred = g.K;
-      po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * kBN;
+      po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * BN;
       ldo = g.N;
     } else {  // kDx
       pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
       lda = g.N;
-      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * kBN * g.N;
+      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
       ldb = g.N;
-      cols_valid = g.K - (int64_t)nt * kBN;
+      cols_valid = g.K - (int64_t)nt * BN;
       kred = g.N;
-      po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * kBN;
+      po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * BN;
       ldo = g.K;
     }
   }
@@ -285,11 +343,11 @@ gg_mfma_kernel(GemmArgs g) {
   const int wave = threadIdx.x / kWave;
   const int wm = wave >> 1, wn = wave & 1;
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
@@ -302,47 +360,94 @@ gg_mfma_kernel(GemmArgs g) {
   if (nk > 0) {
     la.load(pa, lda, rows_valid, kred);
     lb.load(pb, ldb, cols_valid, kred);
+    la.store(smem);
+    lb.store(smem + kStageA);
   }
+  __syncthreads();
   typedef typename mfma_op<T>::vec vec;
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-    la.store(s_a);
-    lb.store(s_b);
-    __syncthreads();
-    if (kt + 1 < nk) {
-      const int64_t kleft = kred - (kt + 1) * kBK;
-      la.load(pa + (kt + 1) * a_kstep, lda, rows_valid, kleft);
-      lb.load(pb + (kt + 1) * b_kstep, ldb, cols_valid, kleft);
-    }
+  // Fragments for k-step ks+1 are read from LDS while the MFMAs of k-step
+  // ks run (two register sets), hiding LDS latency inside one wave.
+  auto compute = [&](const uint16_t* sa, const uint16_t* sb) {
+    const uint16_t* pa_l = sa + (wm * WM + (lane & 31)) * kLdsStride + (lane >> 5) * 8;
+    const uint16_t* pb_l = sb + (wn * WN + (lane & 31)) * kLdsStride + (lane >> 5) * 8;
+    vec av[2][TM], bv[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const vec*>(pa_l + i * 32 * kLdsStride);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[0][j] = *reinterpret_cast<const vec*>(pb_l + j * 32 * kLdsStride);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      vec av[2], bv[2];
-      const int kof = ks * 16 + (lane >> 5) * 8;
+      const int cur = ks & 1;
+      if (ks + 1 < kBK / 16) {
+        const int kof = (ks + 1) * 16;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        av[i] = *reinterpret_cast<const vec*>(s_a + (wm * 64 + i * 32 + (lane & 31)) * kLdsStride + kof);
+        for (int i = 0; i < TM; ++i)
+          av[cur ^ 1][i] = *reinterpret_cast<const vec*>(pa_l + i * 32 * kLdsStride + kof);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bv[j] = *reinterpret_cast<const vec*>(s_b + (wn * 64 + j * 32 + (lane & 31)) * kLdsStride + kof);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_op<T>::run(av[i], bv[j], acc[i][j]);
-    }
-  }
-
-  // Epilogue: acc[i][j][v] holds C[row][col] with col = lane % 32 and
-  // row = 8*(v/4) + 4*(lane/32) + v%4 inside the 32x32 sub-tile.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int col = wn * 64 + j * 32 + (lane & 31);
-        if (row < rows_valid && col < cols_valid) po[(int64_t)row * ldo + col] = cvt_out<T>(acc[i][j][v]);
+        for (int j = 0; j < TN; ++j)
+          bv[cur ^ 1][j] = *reinterpret_cast<const vec*>(pb_l + j * 32 * kLdsStride + kof);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_op<T>::run(bv[cur][j], av[cur][i], acc[i][j]);
+      // Keep each k-step's reads ahead of its MFMAs, and the MFMAs of step
+      // ks ahead of the reads for step ks+2 (no reordering across).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Steady state (branch-free body): load tile kt+1 into registers, compute
+  // tile kt from LDS, store tile kt+1 into the other LDS stage, one barrier.
+  for (int64_t kt = 0; kt + 1 < nk; ++kt) {
+    const int64_t kleft = kred - (kt + 1) * kBK;
+    // The next tile's buffer loads go out first; their latency is covered
+    // by this tile's MFMAs, and the LDS stores come after them.
+    la.load(pa + (kt + 1) * a_kstep, lda, rows_valid, kleft);
+    lb.load(pb + (kt + 1) * b_kstep, ldb, cols_valid, kleft);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* sa = smem + (kt & 1) * kStage;
+    compute(sa, sa + kStageA);
+    uint16_t* nxt = smem + ((kt + 1) & 1) * kStage;
+    la.store(nxt);
+    lb.store(nxt + kStageA);
+    __syncthreads();
+  }
+  if (nk > 0) {
+    const uint16_t* sa = smem + ((nk - 1) & 1) * kStage;
+    compute(sa, sa + kStageA);
+  }
+  __syncthreads();
+
+  // Epilogue. acc[i][j][v] = C[m][n] with m = wm*WM + 32i + lane%32 and
+  // n = wn*WN + 32j + 8*(v/4) + 4*(lane/32) + v%4: each lane packs 4
+  // consecutive columns into 8 bytes of the LDS staging tile.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int m = wm * WM + i * 32 + (lane & 31);
+        const int n = wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
+        uint2 pk;
+        pk.x = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 0]) |
+               ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 1]) << 16);
+        pk.y = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 2]) |
+               ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 3]) << 16);
+        *reinterpret_cast<uint2*>(smem + m * kEpiStride + n) = pk;
+      }
+  __syncthreads();
+  constexpr int kChunksPerRow = BN / 8;
+#pragma unroll 4
+  for (int q = threadIdx.x; q < BM * kChunksPerRow; q += kGemmThreads) {
+    const int row = q / kChunksPerRow;
+    const int c = (q % kChunksPerRow) * 8;
+    if (row < rows_valid && c < cols_valid)
+      *reinterpret_cast<uint4*>(po + (int64_t)row * ldo + c) =
+          *reinterpret_cast<const uint4*>(smem + row * kEpiStride + c);
+  }
 }
 
 // ------------------------------------------------------- generic FMA kernel
@@ -476,33 +581,59 @@ bool mfma_ok(int dtype, int64_t K, int64_t N, const void* p0, const void* p1, co
   return al % 16 == 0;
 }
 
+template <int MODE, int BM, int BN>
+int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
+  g.ntn = (int32_t)ceil_div(out_cols, BN);
+  if (MODE == kDw) {
+    g.ntm = (int32_t)ceil_div(g.K, BM);
+    g.mtiles = (int64_t)g.E * g.ntm;
+  } else {
+    g.ntm = 0;
+    g.mtiles = ceil_div(g.A, BM) + g.E;
+  }
+  const int64_t nblocks = g.mtiles * g.ntn;
+  if (nblocks == 0) return NT_OK;
+  if (nblocks > INT32_MAX) return NT_ERR_TOO_LARGE;
+  const dim3 grid((unsigned)nblocks);
+  if (dtype == NT_BF16)
+    hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE, BM, BN>), grid, dim3(kGemmThreads), 0, s, g);
+  else
+    hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE, BM, BN>), grid, dim3(kGemmThreads), 0, s, g);
+  return launch_status();
+}
+
+// Tile shape: 256x256 when the problem has enough tiles to fill the 256 CUs
+// a few times over, otherwise smaller tiles for more parallelism.
+template <int MODE>
+int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
+  const int64_t rows = MODE == kDw ? g.K * g.E : g.A;
+  auto tiles = [&](int bm, int bn) { return ceil_div(rows, bm) * ceil_div(out_cols, bn); };
+  if (tiles(256, 256) >= 1024) return launch_mfma<MODE, 256, 256>(dtype, g, out_cols, s);
+  if (tiles(256, 128) >= 768) return launch_mfma<MODE, 256, 128>(dtype, g, out_cols, s);
+  return launch_mfma<MODE, 128, 128>(dtype, g, out_cols, s);
+}
+
 template <int MODE>
 int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t s) {
-  const int tile = mfma ? kBM : kGT;
-  const int tile_n = mfma ? kBN : kGT;
-  g.ntn = (int32_t)ceil_div(out_cols, tile_n);
+  if (mfma) return launch_mfma_auto<MODE>(dtype, g, out_cols, s);
+  g.ntn = (int32_t)ceil_div(out_cols, kGT);
   int64_t nblocks;
   if (MODE == kDw) {
-    g.ntm = (int32_t)ceil_div(g.K, tile);
+    g.ntm = (int32_t)ceil_div(g.K, kGT);
     nblocks = (int64_t)g.E * g.ntm * g.ntn;
   } else {
     g.ntm = 0;
-    nblocks = (ceil_div(g.A, tile) + g.E) * (int64_t)g.ntn;
+    nblocks = (ceil_div(g.A, kGT) + g.E) * (int64_t)g.ntn;
   }
   if (nblocks == 0) return NT_OK;
   if (nblocks > INT32_MAX) return NT_ERR_TOO_LARGE;
   const dim3 grid((unsigned)nblocks);
-  if (mfma) {
-    if (dtype == NT_BF16) hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE>), grid, dim3(kGemmThreads), 0, s, g);
-    else hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE>), grid, dim3(kGemmThreads), 0, s, g);
-  } else {
-    switch (dtype) {
-      case NT_F32: hipLaunchKernelGGL((gg_generic_kernel<float, MODE>), grid, dim3(256), 0, s, g); break;
-      case NT_F64: hipLaunchKernelGGL((gg_generic_kernel<double, MODE>), grid, dim3(256), 0, s, g); break;
-      case NT_F16: hipLaunchKernelGGL((gg_generic_kernel<f16, MODE>), grid, dim3(256), 0, s, g); break;
-      case NT_BF16: hipLaunchKernelGGL((gg_generic_kernel<bf16, MODE>), grid, dim3(256), 0, s, g); break;
-      default: return NT_ERR_DTYPE;
-    }
+  switch (dtype) {
+    case NT_F32: hipLaunchKernelGGL((gg_generic_kernel<float, MODE>), grid, dim3(256), 0, s, g); break;
+    case NT_F64: hipLaunchKernelGGL((gg_generic_kernel<double, MODE>), grid, dim3(256), 0, s, g); break;
+    case NT_F16: hipLaunchKernelGGL((gg_generic_kernel<f16, MODE>), grid, dim3(256), 0, s, g); break;
+    case NT_BF16: hipLaunchKernelGGL((gg_generic_kernel<bf16, MODE>), grid, dim3(256), 0, s, g); break;
+    default: return NT_ERR_DTYPE;
   }
   return launch_status();
 }
@@ -543,7 +674,7 @@ int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void
   int st = check_gemm(dtype, E, A, K, N, X, W, offsets, out);
   if (st != NT_OK) return st;
   if (A == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0};
+  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0, 0};
   return launch_mode<kFwd>(dtype, g, N, mfma_ok(dtype, K, N, X, W, out), stream);
 }
 
@@ -555,7 +686,7 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
   int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
   if (st != NT_OK) return st;
   if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0};
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0};
   return launch_mode<kDx>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
 }
 
@@ -567,7 +698,7 @@ int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const v
   int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
   if (st != NT_OK) return st;
   if (K == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0};
+  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0};
   return launch_mode<kDw>(dtype, g, N, mfma_ok(dtype, K, N, X, dOut, dW), stream);
 }
 
