@@ -29,9 +29,10 @@
  *   csrc/bindings.cpp:43-47,82  grouped_gemm_kernel       -> nt_grouped_gemm
  *   csrc/bindings.cpp:53-57,88  bwd_grouped_gemm_dX_kernel-> nt_grouped_gemm_dx
  *   csrc/bindings.cpp:48-52,84  bwd_grouped_gemm_dW_kernel-> nt_grouped_gemm_dw
- * plus the torch glue of src/model/cuda_backend.py:46-67 (count, cumsum,
- * pack) fused into nt_dispatch, and inverse-map variants of combine and pack
- * backward used by the MoE layer.
+ * plus the torch glue of src/model/cuda_backend.py:30-37 (softmax, top-k,
+ * renorm) as nt_route_topk, the glue of :46-67 (count, cumsum, pack) fused
+ * into nt_dispatch, and inverse-map variants of combine and pack backward
+ * used by the MoE layer.
  */
 #ifndef NANOTITAN_MOE_H
 #define NANOTITAN_MOE_H
@@ -159,6 +160,22 @@ int nt_pack_backward(int dtype, const void* dpX, const float* dpw, const int32_t
 int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int32_t* inv,
                          int64_t T, int32_t k, int64_t d, void* dX, float* dw,
                          hipStream_t stream);
+
+/* -------------------------------------------------------------------- router */
+
+/* Router gate for logits [T,E] f32: top-k experts by logit (ties to the
+ * lower expert id; equal to the top-k of softmax(logits)), gates [T,k] f32 =
+ * the softmax of the k selected logits (= the selected probabilities
+ * renormalised to sum 1), topk [T,k] i32 in descending order, and optionally
+ * probs [T,E] = softmax(logits) (NULL to skip). k <= 32.
+ * Replaces the torch glue of reference src/model/cuda_backend.py:30-37. */
+int nt_route_topk(const float* logits, int64_t T, int32_t E, int32_t k, float* gates,
+                  int32_t* topk, float* probs, hipStream_t stream);
+
+/* Gradient of nt_route_topk's gates: dlogits [T,E] f32, zero except at the
+ * selected experts, where dlogits = gate * (dgate - sum_j dgate_j * gate_j). */
+int nt_route_topk_backward(const float* gates, const int32_t* topk, const float* dgates,
+                           int64_t T, int32_t E, int32_t k, float* dlogits, hipStream_t stream);
 
 /* ------------------------------------------------------------- grouped GEMM */
 

@@ -30,7 +30,7 @@ BUILD_DIR = PKG / "_build"
 LIB = PKG / "libnanotitan_moe.so"
 EXT = PKG / "_nanotitan_hip.so"
 
-HIP_SOURCES = ["library.hip", "dispatch.hip", "combine.hip", "grouped_gemm.hip"]
+HIP_SOURCES = ["library.hip", "router.hip", "dispatch.hip", "combine.hip", "grouped_gemm.hip"]
 OFFLOAD_ARCH = "gfx950"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 

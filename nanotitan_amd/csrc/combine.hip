@@ -7,11 +7,12 @@
 // order bit for bit (products are rounded before the add: no FMA).
 //
 // The rows of a token come either from the inverse map written by the pack
-// (inv[t*k + j] = packed slot of token t's j-th choice) or, on the
-// reference's token-id surface, from a token CSR built here: count rows per
-// token, exclusive scan, fill. The fill claims slots with integer atomics, so
-// each token's list is sorted in LDS before use (lists of up to kMaxSorted
-// rows; a longer list is summed in fill order).
+// (inv[t*k + j] = packed slot of token t's j-th choice; the k slots are put
+// in ascending order in LDS) or, on the reference's token-id surface, from a
+// token CSR built here: rows per token (integer atomics) and their exclusive
+// scan give each token's segment, and a stable LSD radix sort of the packed
+// rows by token id (8-bit digits, workgroup-stable ranks from wave ballots)
+// lays every segment out in ascending packed order, for any fan-in.
 #include <algorithm>
 
 #include "common.hpp"
@@ -57,10 +58,11 @@ struct ListSrc {
   int64_t rows;          // packed rows; entries outside [0, rows) are skipped
 };
 
-// Gathers the packed rows of token t into s_out (wave-private LDS of
-// kMaxSorted ints) in ascending order and returns their count, or, for a list
-// longer than kMaxSorted, returns -(length) and leaves the caller to walk it
-// unsorted.
+// Packed rows of token t in ascending order. A CSR list is already sorted
+// and is walked in place: returns -(length). An inverse-map row is compacted
+// (dropping empty slots) and sorted into s_out (wave-private LDS of
+// kMaxSorted ints): returns its count; a row longer than kMaxSorted (top-k
+// above 256) is walked in place, in slot order.
 __device__ int gather_sorted(const ListSrc& src, int64_t t, int32_t* s_in, int32_t* s_out,
                              int64_t* first) {
   const int lane = lane_id();
@@ -68,10 +70,11 @@ __device__ int gather_sorted(const ListSrc& src, int64_t t, int32_t* s_in, int32
   if (src.start != nullptr) {
     b = src.start[t];
     n = src.start[t + 1] - b;
-  } else {
-    b = t * src.k;
-    n = src.k;
+    *first = b;
+    return -(int)n;
   }
+  b = t * src.k;
+  n = src.k;
   *first = b;
   if (n > kMaxSorted) return -(int)n;
   // Compact valid (>= 0) entries into s_in.
@@ -156,15 +159,83 @@ token_scan_kernel(int32_t* __restrict__ cnt, int64_t T, int32_t* __restrict__ st
   if (threadIdx.x == 0) start[T] = s_carry;
 }
 
-__global__ void token_fill_kernel(const int32_t* __restrict__ token_id, int64_t A, int64_t T,
-                                  const int32_t* __restrict__ start, int32_t* __restrict__ cur,
-                                  int32_t* __restrict__ list) {
-  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < A;
-       p += (int64_t)gridDim.x * blockDim.x) {
-    const int32_t t = token_id[p];
-    if (t >= 0 && t < T) {
-      const int slot = atomicAdd(&cur[t], 1);
-      list[start[t] + slot] = (int32_t)p;
+// Stable LSD radix sort of the packed rows by token id, 8 bits per pass.
+// Keys outside [0, T) are mapped to T and sort last (outside every segment).
+constexpr int kRadixBits = 8;
+constexpr int kRadixBins = 1 << kRadixBits;
+constexpr int kRadixChunk = 1024;  // rows per workgroup
+
+__device__ __forceinline__ int radix_key(int32_t v, int64_t T) {
+  return (v >= 0 && v < T) ? v : (int)T;
+}
+
+__global__ void __launch_bounds__(256)
+radix_hist_kernel(const int32_t* __restrict__ keys, int64_t n, int64_t T, int shift, int32_t nb,
+                  int32_t* __restrict__ hist) {
+  __shared__ int32_t s_h[kRadixBins];
+  s_h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t i0 = (int64_t)blockIdx.x * kRadixChunk;
+  for (int r = threadIdx.x; r < kRadixChunk; r += 256) {
+    const int64_t i = i0 + r;
+    if (i < n) atomicAdd(&s_h[(radix_key(keys[i], T) >> shift) & (kRadixBins - 1)], 1);
+  }
+  __syncthreads();
+  hist[(int64_t)threadIdx.x * nb + blockIdx.x] = s_h[threadIdx.x];
+}
+
+// One workgroup: exclusive scan in place of hist[0..count) (digit-major).
+__global__ void __launch_bounds__(1024)
+radix_scan_kernel(int32_t* __restrict__ hist, int64_t count) {
+  __shared__ int32_t s_wsum[16];
+  __shared__ int32_t s_carry;
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (int64_t s0 = 0; s0 < count; s0 += 1024) {
+    const int64_t i = s0 + threadIdx.x;
+    const int v = i < count ? hist[i] : 0;
+    const int incl = wave_incl_scan(v);
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    int before = s_carry;
+    for (int w = 0; w < wave; ++w) before += s_wsum[w];
+    if (i < count) hist[i] = before + incl - v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int tot = 0;
+      for (int w = 0; w < 16; ++w) tot += s_wsum[w];
+      s_carry += tot;
+    }
+    __syncthreads();
+  }
+}
+
+// vals_in == nullptr: the values are the row indices themselves.
+__global__ void __launch_bounds__(256)
+radix_scatter_kernel(const int32_t* __restrict__ keys_in, const int32_t* __restrict__ vals_in,
+                     int64_t n, int64_t T, int shift, int32_t nb,
+                     const int32_t* __restrict__ hist, int32_t* __restrict__ keys_out,
+                     int32_t* __restrict__ vals_out) {
+  __shared__ int32_t s_base[kRadixBins];
+  __shared__ int32_t s_run[kRadixBins];
+  __shared__ int32_t s_wc[4 * kRadixBins];
+  s_base[threadIdx.x] = hist[(int64_t)threadIdx.x * nb + blockIdx.x];
+  s_run[threadIdx.x] = 0;
+  for (int i = threadIdx.x; i < 4 * kRadixBins; i += 256) s_wc[i] = 0;
+  __syncthreads();
+  const int64_t i0 = (int64_t)blockIdx.x * kRadixChunk;
+  for (int r = 0; r < kRadixChunk; r += 256) {
+    const int64_t i = i0 + r + threadIdx.x;
+    const bool valid = i < n;
+    const int key = valid ? radix_key(keys_in[i], T) : 0;
+    const int digit = (key >> shift) & (kRadixBins - 1);
+    const int q = block_rank_round(digit, valid, kRadixBits, kRadixBins, s_run, s_wc);
+    if (valid) {
+      const int64_t pos = s_base[digit] + q;
+      keys_out[pos] = key;
+      vals_out[pos] = vals_in != nullptr ? vals_in[i] : (int32_t)i;
     }
   }
 }
@@ -172,8 +243,22 @@ __global__ void token_fill_kernel(const int32_t* __restrict__ token_id, int64_t 
 struct CsrWs {
   int32_t* cnt;    // [T]
   int32_t* start;  // [T+1]
-  int32_t* list;   // [A]
+  int32_t* keys[2];  // [A] each
+  int32_t* vals[2];  // [A] each
+  int32_t* hist;   // [256 * nb]
 };
+
+int radix_passes(int64_t T) {
+  int bits = 1;
+  while (bits < 62 && ((int64_t)1 << bits) <= T) ++bits;  // T itself must fit (sentinel)
+  return (bits + kRadixBits - 1) / kRadixBits;
+}
+
+size_t csr_bytes(int64_t A, int64_t T) {
+  const int64_t nb = ceil_div(std::max<int64_t>(A, 1), kRadixChunk);
+  return (size_t)(round_up(T * 4, 256) + round_up((T + 1) * 4, 256) + 4 * round_up(A * 4, 256) +
+                  round_up(kRadixBins * nb * 4, 256));
+}
 
 CsrWs carve_csr(void* ws, int64_t A, int64_t T) {
   char* c = static_cast<char*>(ws);
@@ -182,23 +267,49 @@ CsrWs carve_csr(void* ws, int64_t A, int64_t T) {
   c += round_up(T * 4, 256);
   r.start = reinterpret_cast<int32_t*>(c);
   c += round_up((T + 1) * 4, 256);
-  r.list = reinterpret_cast<int32_t*>(c);
+  for (int i = 0; i < 2; ++i) {
+    r.keys[i] = reinterpret_cast<int32_t*>(c);
+    c += round_up(A * 4, 256);
+    r.vals[i] = reinterpret_cast<int32_t*>(c);
+    c += round_up(A * 4, 256);
+  }
+  r.hist = reinterpret_cast<int32_t*>(c);
   return r;
 }
 
-size_t csr_bytes(int64_t A, int64_t T) {
-  return (size_t)(round_up(T * 4, 256) + round_up((T + 1) * 4, 256) + round_up(A * 4, 256));
-}
-
-int build_csr(const int32_t* token_id, int64_t A, int64_t T, const CsrWs& c, hipStream_t s) {
+// Builds start[0..T] and returns the sorted list (rows of each token in
+// ascending packed order) through *list.
+int build_csr(const int32_t* token_id, int64_t A, int64_t T, const CsrWs& c, const int32_t** list,
+              hipStream_t s) {
   const int grid_t = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(T, 1), 256), 4096);
   const int grid_a = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(A, 1), 256), 4096);
   hipLaunchKernelGGL(zero_i32, dim3(grid_t), dim3(256), 0, s, c.cnt, T);
   hipLaunchKernelGGL(token_count_kernel, dim3(grid_a), dim3(256), 0, s, token_id, A, T, c.cnt);
   hipLaunchKernelGGL(token_scan_kernel, dim3(1), dim3(1024), 0, s, c.cnt, T, c.start);
-  hipLaunchKernelGGL(token_fill_kernel, dim3(grid_a), dim3(256), 0, s, token_id, A, T, c.start,
-                     c.cnt, c.list);
-  return launch_status();
+  int st = launch_status();
+  if (st != NT_OK) return st;
+  *list = nullptr;
+  if (A == 0) return NT_OK;
+  const int32_t nb = (int32_t)ceil_div(A, kRadixChunk);
+  const int passes = radix_passes(T);
+  const int32_t* kin = token_id;
+  const int32_t* vin = nullptr;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = pass * kRadixBits;
+    int32_t* kout = c.keys[pass & 1];
+    int32_t* vout = c.vals[pass & 1];
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(nb), dim3(256), 0, s, kin, A, T, shift, nb, c.hist);
+    hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(1024), 0, s, c.hist,
+                       (int64_t)kRadixBins * nb);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3(nb), dim3(256), 0, s, kin, vin, A, T, shift, nb,
+                       c.hist, kout, vout);
+    st = launch_status();
+    if (st != NT_OK) return st;
+    kin = kout;
+    vin = vout;
+  }
+  *list = vin;
+  return NT_OK;
 }
 
 // ------------------------------------------------------------- combine fwd
@@ -552,9 +663,10 @@ int nt_combine_tokens(int dtype, const void* y, const int32_t* token_id, const f
   if (ws == nullptr || ws_bytes < csr_bytes(A, T)) return NT_ERR_WORKSPACE;
   if (T == 0) return NT_OK;
   const CsrWs c = carve_csr(ws, A, T);
-  int st = build_csr(token_id, A, T, c, stream);
+  const int32_t* list = nullptr;
+  int st = build_csr(token_id, A, T, c, &list, stream);
   if (st != NT_OK) return st;
-  ListSrc src{c.start, c.list, 0, A};
+  ListSrc src{c.start, list, 0, A};
   return combine_dispatch(dtype, NT_F32, y, src, w, T, d, out, stream);
 }
 
@@ -625,9 +737,10 @@ int nt_pack_backward(int dtype, const void* dpX, const float* dpw, const int32_t
   if (ws == nullptr || ws_bytes < csr_bytes(A, T)) return NT_ERR_WORKSPACE;
   if (T == 0) return NT_OK;
   const CsrWs c = carve_csr(ws, A, T);
-  int st = build_csr(token_id, A, T, c, stream);
+  const int32_t* list = nullptr;
+  int st = build_csr(token_id, A, T, c, &list, stream);
   if (st != NT_OK) return st;
-  ListSrc src{c.start, c.list, 0, A};
+  ListSrc src{c.start, list, 0, A};
   return pack_bwd_dispatch(dtype, dpX, dpw, src, expert, topk, T, k, d, dX, dw, stream);
 }
 

@@ -128,6 +128,45 @@ __device__ __forceinline__ void lds_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// One round of a workgroup-wide stable counting rank. Every thread of the
+// workgroup passes one item (key in [0, nkeys) when valid); the result is the
+// number of valid items with the same key that precede it in thread order in
+// this round plus in all earlier rounds (s_run[nkeys] carries those counts and
+// is updated; s_wc[waves][nkeys] is scratch, zero on entry and on exit).
+// Peers with equal keys inside a wave are found with one ballot per key bit.
+// Contains workgroup barriers: all threads must call it. Returns -1 for an
+// invalid item.
+__device__ __forceinline__ int block_rank_round(int key, bool valid, int nbits, int nkeys,
+                                                int32_t* s_run, int32_t* s_wc) {
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = blockDim.x / kWave;
+  uint64_t peers = ballot(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool set = valid && ((key >> bit) & 1);
+    const uint64_t bb = ballot(set);
+    peers &= set ? bb : ~bb;
+  }
+  const int rank_w = popc64(peers & lanemask_lt());
+  if (valid && rank_w == 0) s_wc[wave * nkeys + key] = popc64(peers);
+  __syncthreads();
+  int q = -1;
+  if (valid) {
+    q = s_run[key] + rank_w;
+    for (int w2 = 0; w2 < wave; ++w2) q += s_wc[w2 * nkeys + key];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nkeys; e += blockDim.x) {
+    int add = 0;
+    for (int w2 = 0; w2 < nwaves; ++w2) {
+      add += s_wc[w2 * nkeys + e];
+      s_wc[w2 * nkeys + e] = 0;
+    }
+    s_run[e] += add;
+  }
+  __syncthreads();
+  return q;
+}
+
 // Round a non-negative size up to a multiple of a.
 __host__ __device__ constexpr int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 __host__ __device__ constexpr int64_t ceil_div(int64_t x, int64_t a) { return (x + a - 1) / a; }

@@ -171,38 +171,19 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
   // Stable rank of each assignment among same-expert assignments of the block.
   for (int r = 0; r < na; r += kDispatchThreads) {
     const int i = r + tid;
-    int32_t e = i < na ? topk[f0 + i] : -1;
+    const int32_t e = i < na ? topk[f0 + i] : -1;
     const bool valid = e >= 0 && e < E;
-    uint64_t peers = ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool set = valid && ((e >> bit) & 1);
-      const uint64_t bb = ballot(set);
-      peers &= set ? bb : ~bb;
-    }
-    const int rank_w = popc64(peers & lanemask_lt());
-    if (valid && rank_w == 0) s_wc[wave * E + e] = popc64(peers);
-    __syncthreads();
+    const int q = block_rank_round(e, valid, nbits, E, s_run, s_wc);
     if (i < na) {
       int32_t p = -1;
       if (valid) {
-        int q = s_run[e] + rank_w;
-        for (int w2 = 0; w2 < wave; ++w2) q += s_wc[w2 * E + e];
         p = s_base[e] + q;
         if (p < 0 || (int64_t)p >= A_cap) p = -1;
       }
       s_pos[i] = p;
     }
-    __syncthreads();
-    for (int e2 = tid; e2 < E; e2 += kDispatchThreads) {
-      int add = 0;
-      for (int w2 = 0; w2 < kDispatchWaves; ++w2) {
-        add += s_wc[w2 * E + e2];
-        s_wc[w2 * E + e2] = 0;
-      }
-      s_run[e2] += add;
-    }
-    __syncthreads();
   }
+  __syncthreads();  // s_pos complete before other threads read it
 
   // Metadata: one thread per assignment.
   for (int i = tid; i < na; i += kDispatchThreads) {

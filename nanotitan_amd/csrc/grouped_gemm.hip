@@ -42,12 +42,10 @@ __device__ __forceinline__ void expert_rows(const int32_t* __restrict__ offsets,
   r1 = b;
 }
 
-// Maps m-tile index `mt_global` (over all experts, expert-major) to its
-// expert. s_pref[e] = number of m-tiles of experts < e; built cooperatively.
-// Returns false when mt_global is past the last tile.
-__device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A, int BM,
-                           int64_t mt_global, int32_t* s_pref, int& e_out, int64_t& r0,
-                           int64_t& r1, int64_t& mt_local) {
+// s_pref[e] = number of BM-row tiles of experts < e (s_pref[E] = total),
+// built by the first wave; ends with a workgroup barrier.
+__device__ void build_m_prefix(const int32_t* __restrict__ offsets, int E, int64_t A, int BM,
+                               int32_t* s_pref) {
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
     int carry = 0;
@@ -66,6 +64,13 @@ __device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A
     if (lane == 0) s_pref[0] = 0;
   }
   __syncthreads();
+}
+
+// Expert owning m-tile `mt_global` (expert-major order) and the tile's row
+// range; false when mt_global is past the last tile.
+__device__ bool find_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A,
+                            const int32_t* s_pref, int64_t mt_global, int& e_out, int64_t& r0,
+                            int64_t& r1, int64_t& mt_local) {
   if (mt_global >= s_pref[E]) return false;
   int lo = 0, hi = E - 1;  // largest e with s_pref[e] <= mt_global
   while (lo < hi) {
@@ -73,12 +78,17 @@ __device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A
     if (s_pref[mid] <= mt_global) lo = mid;
     else hi = mid - 1;
   }
-  // Skip experts with zero tiles that share the same prefix value.
-  while (lo < E - 1 && s_pref[lo + 1] <= mt_global) ++lo;
   e_out = lo;
   expert_rows(offsets, lo, A, r0, r1);
   mt_local = mt_global - s_pref[lo];
   return true;
+}
+
+__device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A, int BM,
+                           int64_t mt_global, int32_t* s_pref, int& e_out, int64_t& r0,
+                           int64_t& r1, int64_t& mt_local) {
+  build_m_prefix(offsets, E, A, BM, s_pref);
+  return find_m_tile(offsets, E, A, s_pref, mt_global, e_out, r0, r1, mt_local);
 }
 
 // ------------------------------------------------------- MFMA operand tiles
@@ -261,7 +271,10 @@ __device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int
   nt = (int)(rem / gsz);
 }
 
-// One BM x BN output tile per workgroup of 4 waves (2 x 2); each wave owns a
+// Persistent: one or two workgroups per CU loop over output tiles. Tiles are
+// dealt to XCDs in contiguous ranges (neighbouring tiles share operand panels
+// in that XCD's L2), and a tile's output stores drain while the next tile
+// computes. Each tile is BM x BN, computed by 4 waves (2 x 2); each wave owns a
 // (BM/2) x (BN/2) block of 32x32 MFMA tiles. The MFMA is issued with the B
 // fragment as its first operand, so each lane's accumulator holds 4
 // consecutive output columns of one output row (packable 8-byte groups).
@@ -286,16 +299,34 @@ gg_mfma_kernel(GemmArgs g) {
   typedef typename LoaderSel<kAK, BM>::type LA;
   typedef typename LoaderSel<kBK_, BN>::type LB;
 
+  int64_t mtiles = g.mtiles;
+  if (MODE != kDw) {
+    build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
+    mtiles = s_pref[g.E];
+  }
+  const int64_t total = mtiles * g.ntn;
+  // Blocks are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8).
+  // XCD x owns a contiguous range of tiles, sized by how many blocks it has;
+  // its blocks walk that range in step. With one tile per block (large
+  // tiles, non-persistent launch) this reduces to a renumbering.
+  constexpr int kXcd = 8;
+  const int64_t G = gridDim.x;
+  const int xcd = blockIdx.x % kXcd;
+  const int64_t q = G / kXcd, r = G % kXcd;
+  const int64_t before = xcd * q + (xcd < r ? xcd : r);
+  const int64_t nbx = q + (xcd < r ? 1 : 0);
+  const int64_t t_end = total * (before + nbx) / G;
+  for (int64_t logical = total * before / G + blockIdx.x / kXcd; logical < t_end;
+       logical += nbx) {
   const uint16_t* pa;
   const uint16_t* pb;
   int64_t lda, ldb, rows_valid, cols_valid, kred;
   uint16_t* po;
   int64_t ldo;
 
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
   int64_t mt;
   int nt;
-  tile_coords(logical, g.mtiles, g.ntn, mt, nt);
+  tile_coords(logical, mtiles, g.ntn, mt, nt);
 
   if (MODE == kDw) {
     const int e = (int)(mt / g.ntm);
@@ -315,7 +346,7 @@ gg_mfma_kernel(GemmArgs g) {
   } else {
     int e;
     int64_t r0, r1, mtl;
-    if (!map_m_tile(g.offsets, g.E, g.A, BM, mt, s_pref, e, r0, r1, mtl)) return;
+    find_m_tile(g.offsets, g.E, g.A, s_pref, mt, e, r0, r1, mtl);
     const int64_t row0 = r0 + mtl * BM;
     rows_valid = r1 - row0;
     if (MODE == kFwd) {
@@ -447,6 +478,11 @@ gg_mfma_kernel(GemmArgs g) {
     if (row < rows_valid && c < cols_valid)
       *reinterpret_cast<uint4*>(po + (int64_t)row * ldo + c) =
           *reinterpret_cast<const uint4*>(smem + row * kEpiStride + c);
+  }
+  __syncthreads();  // the staging tile is read before the next tile reuses LDS
+  // 256x256 tiles are launched one per workgroup: a single pass, so nothing
+  // is carried (or hoisted) across tiles.
+  if constexpr (BM * BN >= 256 * 256) break;
   }
 }
 
@@ -581,6 +617,21 @@ bool mfma_ok(int dtype, int64_t K, int64_t N, const void* p0, const void* p1, co
   return al % 16 == 0;
 }
 
+// Compute units of the current device (cached per device id).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <int MODE, int BM, int BN>
 int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   g.ntn = (int32_t)ceil_div(out_cols, BN);
@@ -591,9 +642,16 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
     g.ntm = 0;
     g.mtiles = ceil_div(g.A, BM) + g.E;
   }
-  const int64_t nblocks = g.mtiles * g.ntn;
-  if (nblocks == 0) return NT_OK;
-  if (nblocks > INT32_MAX) return NT_ERR_TOO_LARGE;
+  const int64_t tiles = g.mtiles * g.ntn;
+  if (tiles == 0) return NT_OK;
+  if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
+  // 256x256 tiles: one tile per workgroup (a tile loop would push the
+  // 512-register kernel into spills); smaller tiles: persistent workgroups,
+  // one (256x128) or two (128x128) per CU.
+  const int per_cu = BM * BN >= 256 * 128 ? 1 : 2;
+  const int64_t nblocks = BM * BN >= 256 * 256
+                              ? tiles
+                              : std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
   const dim3 grid((unsigned)nblocks);
   if (dtype == NT_BF16)
     hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE, BM, BN>), grid, dim3(kGemmThreads), 0, s, g);

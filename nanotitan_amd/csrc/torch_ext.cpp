@@ -286,6 +286,41 @@ Tensor bwd_grouped_gemm_dX_kernel(Tensor W, Tensor offsets, Tensor dOut) {
 
 // ------------------------------------------------------- layer extensions
 
+// Fused router gate: (gates [T,k] f32, topk [T,k] i32).
+std::tuple<Tensor, Tensor> route_topk(Tensor logits, int64_t k) {
+  TORCH_CHECK(logits.is_contiguous() && logits.dim() == 2, "logits must be a contiguous [T,E]");
+  check_f32(logits, "logits");
+  const int64_t T = logits.size(0), E = logits.size(1);
+  TORCH_CHECK(k >= 1 && k <= E && k <= 32, "top_k must be in [1, min(E, 32)]");
+  c10::hip::HIPGuard guard(logits.get_device());
+  Tensor gates = at::empty({T, k}, logits.options());
+  Tensor topk = at::empty({T, k}, logits.options().dtype(at::kInt));
+  check_status(nt_route_topk(logits.data_ptr<float>(), T, (int32_t)E, (int32_t)k,
+                             gates.data_ptr<float>(), topk.data_ptr<int32_t>(), nullptr,
+                             stream_of(logits)),
+               "route_topk");
+  return {gates, topk};
+}
+
+Tensor route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int64_t num_experts) {
+  TORCH_CHECK(gates.is_contiguous() && topk.is_contiguous() && dgates.is_contiguous(),
+              "inputs must be contiguous");
+  check_f32(gates, "gates");
+  check_f32(dgates, "dgates");
+  check_i32(topk, "topk");
+  TORCH_CHECK(gates.sizes() == topk.sizes() && gates.sizes() == dgates.sizes() &&
+                  gates.dim() == 2,
+              "gates, topk and dgates must all be [T,k]");
+  const int64_t T = gates.size(0), k = gates.size(1);
+  c10::hip::HIPGuard guard(gates.get_device());
+  Tensor dlogits = at::empty({T, num_experts}, gates.options());
+  check_status(nt_route_topk_backward(gates.data_ptr<float>(), topk.data_ptr<int32_t>(),
+                                      dgates.data_ptr<float>(), T, (int32_t)num_experts,
+                                      (int32_t)k, dlogits.data_ptr<float>(), stream_of(gates)),
+               "route_topk_backward");
+  return dlogits;
+}
+
 // Fused count + scan + pack: (counts [E], offsets [E+1], packed_X, token_id,
 // expert, packed_w, inv [T,k]).
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens(
@@ -411,5 +446,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("combine_inv", &combine_inv, "Combine driven by the inverse map");
   m.def("combine_backward_inv", &combine_backward_inv, "Combine backward driven by the inverse map");
   m.def("pack_backward_inv", &pack_backward_inv, "Pack backward driven by the inverse map");
+  m.def("route_topk", &route_topk, "Fused softmax / top-k / renorm router gate -> (gates, topk)");
+  m.def("route_topk_backward", &route_topk_backward, "Gradient of route_topk's gates -> dlogits");
   m.def("version", []() { return nt_version(); });
 }

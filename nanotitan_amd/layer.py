@@ -27,7 +27,7 @@ import torch
 import torch.nn as nn
 from torch.profiler import record_function
 
-from nanotitan_amd.moe_ops import combine_inv_fn, dispatch_fn, grouped_gemm_fn
+from nanotitan_amd.moe_ops import combine_inv_fn, dispatch_fn, grouped_gemm_fn, route_fn
 
 HIP_BACKENDS = ("hip", "cuda")  # "cuda" is accepted so reference configs select this path
 
@@ -70,17 +70,15 @@ class MoELayerStats:
 
 
 def route(logits: torch.Tensor, top_k: int):
-    """(gates f32 [T,k], ids int32 [T,k], probs f32 [T,E]).
+    """(gates f32 [T,k], ids int32 [T,k]) from the fused router kernel.
 
-    Reference src/model/cuda_backend.py:30-37 uses torch.topk, whose order
-    among equal probabilities is unspecified; the stable descending sort
-    here sends ties to the lower expert id.
+    Reference src/model/cuda_backend.py:30-37: fp32 softmax, torch.topk,
+    renormalise. The kernel selects the k largest logits (the same set as the
+    k largest probabilities; ties go to the lower expert id, where torch.topk
+    leaves the order unspecified) and returns the selected probabilities
+    renormalised to sum 1.
     """
-    probs = logits.float().softmax(dim=-1)
-    vals, idx = torch.sort(probs, dim=-1, descending=True, stable=True)
-    vals = vals[:, :top_k]
-    gates = vals / vals.sum(dim=-1, keepdim=True)
-    return gates, idx[:, :top_k].to(torch.int32), probs
+    return route_fn(logits.float().contiguous(), top_k)
 
 
 def _check_backend(cfg):
@@ -134,10 +132,10 @@ class GeluExpertFFN(nn.Module):
 def moe_forward_from_logits(x_flat, logits, experts, num_experts, top_k):
     """Hot path from router logits: route, dispatch, experts, combine (output in x's dtype).
 
-    Returns (out [T,d], counts [E], probs [T,E]).
+    Returns (out [T,d], counts [E], gates [T,k]).
     """
     with record_function("moe/topK"):
-        gates, idx, probs = route(logits, top_k)
+        gates, idx = route(logits, top_k)
     with record_function("moe/pack_tokens"):
         packed_X, packed_w, counts, offsets, _token_id, inv = dispatch_fn(
             x_flat, gates, idx, num_experts
@@ -146,7 +144,7 @@ def moe_forward_from_logits(x_flat, logits, experts, num_experts, top_k):
         y = experts(packed_X, offsets)
     with record_function("moe/combine_tokens"):
         out = combine_inv_fn(y, inv, packed_w, x_flat.dtype)
-    return out, counts, probs
+    return out, counts, gates
 
 
 class HIPMoEBackend:

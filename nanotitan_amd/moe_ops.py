@@ -189,6 +189,37 @@ class CombineInvFN(torch.autograd.Function):
         return dy, None, dw, None
 
 
+class RouteFN(torch.autograd.Function):
+    """Fused router gate: logits [T,E] f32 -> (gates [T,k] f32, topk [T,k] int32).
+
+    Top-k by logit with ties to the lower expert id (the top-k of the
+    softmax probabilities), gates = the selected probabilities renormalised
+    (reference src/model/cuda_backend.py:30-37). Backward returns dlogits.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, top_k):
+        ext = get_hip_extension()
+        gates, topk = ext.route_topk(logits.contiguous(), top_k)
+        ctx.save_for_backward(gates, topk)
+        ctx.num_experts = logits.shape[1]
+        ctx.mark_non_differentiable(topk)
+        return gates, topk
+
+    @staticmethod
+    def backward(ctx, dgates, _dtopk):
+        ext = get_hip_extension()
+        gates, topk = ctx.saved_tensors
+        if dgates is None:
+            return None, None
+        return ext.route_topk_backward(gates, topk, dgates.contiguous().float(),
+                                       ctx.num_experts), None
+
+
+def route_fn(logits, top_k):
+    return RouteFN.apply(logits, top_k)
+
+
 def dispatch_fn(X, topk_weights, topk_experts, num_experts):
     return DispatchFN.apply(X, topk_weights, topk_experts, num_experts)
 

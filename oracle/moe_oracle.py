@@ -49,7 +49,7 @@ PINNING = {
     "grouped_gemm": "torch.autograd of reference test formula (float64)",
     "grouped_gemm_dx": "torch.autograd of reference test formula (float64)",
     "grouped_gemm_dw": "torch.autograd of reference test formula (float64)",
-    "route": "brute-force sort with explicit tie rule",
+    "route": "brute-force sort with explicit tie rule + torch softmax/renorm",
     "moe_layer": "token-by-token dense restatement + torch.autograd",
 }
 
@@ -282,17 +282,29 @@ def grouped_gemm_dw(X, offsets, dOut) -> torch.Tensor:
 # ------------------------------------------------------------------ routing
 
 
-def route(logits: torch.Tensor, top_k: int):
-    """fp32 softmax, stable top-k (ties to the lower expert id), renormalised gates.
+def select_topk(logits: torch.Tensor, top_k: int) -> torch.Tensor:
+    """Indices of the k largest logits per row, ties to the lower expert id.
 
-    Reference: src/model/cuda_backend.py:30-37 (softmax, topk, renorm in
-    fp32). torch.topk leaves tie order unspecified; the stable descending
-    sort fixes it to the lower expert id.
+    The k largest logits are the k largest softmax probabilities (softmax is
+    monotonic); comparing logits avoids ties created by rounding the
+    probabilities. torch.topk, used by the reference
+    (src/model/cuda_backend.py:34), leaves the order of ties unspecified.
+    """
+    _, idx = torch.sort(logits.float(), dim=-1, descending=True, stable=True)
+    return idx[:, :top_k]
+
+
+def route(logits: torch.Tensor, top_k: int):
+    """(gates f32 [T,k], ids int32 [T,k], probs f32 [T,E]).
+
+    Reference: src/model/cuda_backend.py:30-37 (fp32 softmax, top-k,
+    gates = p_topk / sum p_topk). The renormalised gates equal the softmax of
+    the selected logits; computed here in float64 and rounded.
     """
     probs = logits.float().softmax(dim=-1)
-    vals, idx = torch.sort(probs, dim=-1, descending=True, stable=True)
-    vals, idx = vals[:, :top_k], idx[:, :top_k]
-    gates = vals / vals.sum(dim=-1, keepdim=True)
+    idx = select_topk(logits, top_k)
+    sel = torch.gather(logits.double(), 1, idx)
+    gates = sel.softmax(dim=-1).float()
     return gates, idx.to(torch.int32), probs
 
 
@@ -322,8 +334,8 @@ def moe_layer_torch(x, logits, weights, top_k, ffn="gelu", dY=None):
     T, d = x.shape
     E = logits.shape[1]
     probs = logits.float().softmax(dim=-1)
-    vals, idx = torch.sort(probs, dim=-1, descending=True, stable=True)
-    vals, idx = vals[:, :top_k], idx[:, :top_k]
+    idx = select_topk(logits, top_k)
+    vals = torch.gather(probs, 1, idx)
     gates = vals / vals.sum(dim=-1, keepdim=True)
     counts = torch.bincount(idx.reshape(-1), minlength=E)
     offsets = torch.zeros(E + 1, dtype=torch.long)
@@ -370,8 +382,8 @@ def moe_layer_dense(x, logits, weights, top_k, ffn="gelu"):
     moe_layer_torch; differentiable through torch.autograd.
     """
     probs = logits.double().softmax(dim=-1)
-    vals, idx = torch.sort(probs, dim=-1, descending=True, stable=True)
-    vals, idx = vals[:, :top_k], idx[:, :top_k]
+    idx = select_topk(logits.detach(), top_k)
+    vals = torch.gather(probs, 1, idx)
     gates = vals / vals.sum(dim=-1, keepdim=True)
     xd = x.double()
     rows = []
