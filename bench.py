@@ -303,6 +303,17 @@ def main():
         "flops_per_launch": gemm["work"] / max(gemm["launches"], 1),
         "avg_launch_ms": gemm["ms"] / max(gemm["launches"], 1),
     }
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # (calibrated on a device copy), committed with the profile summaries.
+    prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
+    if prof.exists():
+        fams_t = json.loads(prof.read_text()).get("families", {})
+        gemm_t = [fams_t[f] for f in ("gemm_fwd", "gemm_dx", "gemm_dw") if f in fams_t]
+        if gemm_t:
+            roofline["traffic"] = round(sum(t["bytes"] for t in gemm_t) / len(gemm_t))
+            roofline["traffic_algorithmic"] = round(
+                sum(t["algorithmic_bytes"] for t in gemm_t) / len(gemm_t))
+            roofline["traffic_source"] = f"profiles/{prof.name}"
     kernels = {}
     for fam, r in fams.items():
         avg_ms = r["ms"] / r["launches"]
