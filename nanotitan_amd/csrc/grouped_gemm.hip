@@ -27,7 +27,6 @@ namespace {
 
 enum GemmMode { kFwd = 0, kDx = 1, kDw = 2 };
 
-constexpr int kGemmThreads = 256;
 
 // ------------------------------------------------------------ scheduling
 
@@ -96,6 +95,8 @@ __device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
 template <typename T>
 struct mfma_op;
@@ -114,125 +115,158 @@ struct mfma_op<f16> {
   }
 };
 
-constexpr int kBK = 64;
-constexpr int kLdsStride = kBK + 8;  // elements; 144 B rows keep 16-B reads conflict-free
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-// Operand tiles are fetched with raw buffer loads: one wave-uniform
-// descriptor per tile and k-step (base address + byte range), a 32-bit
-// per-lane offset, and the hardware's range check returning zeros for any
-// offset past the range. Lanes whose slot is outside the tile get kOob.
-// No branches or selects around the loads, and no 64-bit address registers.
+constexpr int kBK = 64;            // reduction elements per k-step
+constexpr int kMfmaThreads = 512;  // 8 waves, two per SIMD
+constexpr int kMfmaWaves = kMfmaThreads / kWave;
+
+// Operand tiles are fetched with raw buffer loads that write straight into
+// LDS (buffer_load_dwordx4 ... lds): lane i of one instruction lands at
+// 16*i bytes past the instruction's LDS base (M0), so one instruction fills
+// 1 KiB of LDS and the lane -> global-address map chooses the LDS layout.
+// The descriptor's range check turns any offset past the range into a zero
+// fill; lanes whose chunk lies past the reduction end get kOob.
+//
+// The loads are issued from inline assembly: the compiler then does not
+// treat them as LDS writes that every later LDS read must wait for (it
+// would wait for the next stage's loads before reading the current stage).
+// Completion is explicit instead: s_waitcnt vmcnt(0) and a workgroup
+// barrier before a stage is read.
 constexpr uint32_t kBufConfig = 0x00020000u;  // gfx9 buffer descriptor word 3
 constexpr uint32_t kOob = 0x80000000u;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+__device__ __forceinline__ i32x4_t make_rsrc(const void* base, int64_t bytes) {
   const int32_t n = (int32_t)(bytes <= 0 ? 0 : (bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, (int)kBufConfig);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane(n);
+  r[3] = (int)kBufConfig;
+  return r;
 }
 
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
-  return make_uint4(v[0], v[1], v[2], v[3]);
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)p);
 }
 
-// K-contiguous operand: element (row, kk) at p[row*ld + kk]; `rows` valid
-// rows, `kleft` valid kk from this k-step on. One 16-byte chunk (8 elements
-// along kk) per slot.
-template <int ROWS>
-struct LoaderK {
-  static constexpr int kChunks = ROWS * kBK / 8 / kGemmThreads;
-  static constexpr int kLoads = kChunks;   // buffer loads per tile
-  static constexpr int kStores = kChunks;  // LDS writes per tile
-  uint4 r[kChunks];
-  __device__ void load(const uint16_t* p, int64_t ld, int64_t rows, int64_t kleft) {
-    const int64_t kv = kleft < kBK ? kleft : kBK;
-    const int64_t rv = rows < ROWS ? rows : ROWS;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p, ((rv - 1) * ld + kv) * 2);
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int q = threadIdx.x + i * kGemmThreads;
-      const int row = q / (kBK / 8);
-      const int kc = (q % (kBK / 8)) * 8;
-      const uint32_t off = kc < kv ? (uint32_t)(row * ld + kc) * 2u : kOob;
-      r[i] = buf_load16(rs, off);
+__device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(lds)
+      : "memory", "m0");
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// One operand tile in LDS, ROWS (m or n) x kBK (reduction) 16-bit elements.
+//
+// K-major (the reduction index is contiguous in HBM): row r of the tile is
+// kBK elements = 128 B = 8 chunks of 16 B, chunk c stored at position
+// c ^ ((r >> 1) & 7). An MFMA fragment read (ds_read_b128, 16 lanes per LDS
+// cycle: rows r..r+15, one chunk) then touches all 64 banks once.
+//
+// MN-major (m / n contiguous in HBM): row k of the tile holds ROWS elements
+// (ROWS/8 chunks), chunk c stored at c ^ (4 * (k & 3)). Fragments come from
+// ds_read_b64_tr_b16, which transposes 4x4 blocks of 16-bit elements across
+// each 16-lane group: source lane 4j+q reads the 4 elements at (k0 + j,
+// mn0 + 4q .. 4q+3); destination lane 4q+e receives (k0 + 0..3, mn0 + 4q + e).
+// Two such reads (k0 and k0 + 4) give a lane the 8 consecutive reduction
+// elements of one m / n index that v_mfma_f32_32x32x16 takes. 32 lanes per
+// LDS cycle read 4 rows x 4 chunks, which the XOR spreads over all 64 banks.
+//
+// Wave w issues instructions w, w+8, ...; for a given lane these differ only
+// by a whole number of XOR periods, so one per-lane offset plus a uniform
+// stride per instruction covers them.
+template <int ROWS, bool KMAJ>
+struct OperandTile {
+  static constexpr int kBytes = ROWS * kBK * 2;
+  static constexpr int kInsts = kBytes / 1024;   // 1 KiB per load instruction
+  static constexpr int kPer = kInsts / kMfmaWaves;
+  static_assert(kPer >= 1 && kInsts % kMfmaWaves == 0, "tile too small for 8 waves");
+  static_assert(KMAJ || ROWS >= 128, "MN-major tiles need at least 16 chunks per row");
+  static constexpr int kRowBytes = KMAJ ? kBK * 2 : ROWS * 2;
+  static constexpr int kRowsPerInst = 1024 / kRowBytes;
+
+  uint32_t off;     // byte offset of this lane's chunk (instruction `wave`) from the tile origin
+  uint32_t kchunk;  // K-major: first reduction index of the lane's chunk
+  uint32_t ustep;   // byte stride between this wave's successive instructions
+
+  __device__ void init(int64_t ld, int wave, int lane) {
+    const int t = wave;
+    int r, c;
+    if (KMAJ) {
+      r = 8 * t + (lane >> 3);
+      c = (lane & 7) ^ ((r >> 1) & 7);
+    } else {
+      constexpr int kCpr = ROWS / 8;  // chunks per row
+      r = kRowsPerInst * t + lane / kCpr;
+      c = (lane % kCpr) ^ (4 * (r & 3));
     }
+    off = (uint32_t)((int64_t)r * ld + c * 8) * 2u;
+    kchunk = (uint32_t)(c * 8);
+    ustep = (uint32_t)(kMfmaWaves * kRowsPerInst * ld * 2);
   }
-  __device__ void store(uint16_t* s) const {
+
+  // Issue this wave's share of the tile's loads. `base` is the tile origin
+  // for this k-step; `range` bytes from it are readable; `kv` reduction
+  // elements are valid (K-major chunks past kv are zero-filled; MN-major
+  // rows past kv fall outside `range`).
+  __device__ void issue(const void* base, int64_t range, char* lds, int64_t kv, int wave) const {
+    const i32x4_t rs = make_rsrc(base, range);
+    const uint32_t l0 = lds_addr(lds) + (uint32_t)wave * 1024u;
+    uint32_t v = off;
+    if (KMAJ && kv < kBK && (int64_t)kchunk >= kv) v = kOob;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int q = threadIdx.x + i * kGemmThreads;
-      const int row = q / (kBK / 8);
-      const int kc = (q % (kBK / 8)) * 8;
-      *reinterpret_cast<uint4*>(s + row * kLdsStride + kc) = r[i];
-    }
+    for (int u = 0; u < kPer; ++u)
+      load16_to_lds(rs, v + (uint32_t)u * ustep, l0 + (uint32_t)(u * kMfmaWaves * 1024));
   }
 };
 
-// M-contiguous operand: element (row, kk) at p[kk*ld + row]; `rows` valid
-// rows (columns in memory), `kleft` valid kk. Each slot is a 4 (kk) x 8 (row)
-// block: four 16-byte loads, transposed in registers into eight 8-byte LDS
-// writes (row-major, kk contiguous). Consecutive lanes take consecutive kk
-// blocks of the same rows, so each group of 16 lanes writes 128 contiguous
-// LDS bytes of one row (bank-conflict free); across the wave the four row
-// groups read 64 contiguous bytes of every HBM row they touch.
-template <int ROWS>
-struct LoaderM {
-  static constexpr int kBlocks = ROWS * kBK / 32 / kGemmThreads;
-  static_assert(kBlocks >= 1, "tile too small for one 4x8 block per thread");
-  static constexpr int kLoads = 4 * kBlocks;
-  static constexpr int kStores = 8 * kBlocks;
-  uint4 r[kBlocks][4];
-  __device__ void load(const uint16_t* p, int64_t ld, int64_t rows, int64_t kleft) {
-    const int64_t kv = kleft < kBK ? kleft : kBK;
-    const int64_t cv = rows < ld ? rows : ld;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p, ((kv - 1) * ld + cv) * 2);
+// Per-lane LDS byte offsets of the fragment reads of one operand: TS 32-row
+// sub-tiles starting at row `row0` of the tile, for each of the 4 k-substeps
+// of 16 elements.
+template <int ROWS, bool KMAJ, int TS>
+struct FragReader {
+  static constexpr int kRowBytes = KMAJ ? kBK * 2 : ROWS * 2;
+  uint32_t base[KMAJ ? 4 : TS];
+  __device__ void init(int row0, int lane) {
+    if (KMAJ) {
+      const int r = row0 + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < kBlocks; ++i) {
-      const int q = threadIdx.x + i * kGemmThreads;
-      const int kb = (q % (kBK / 4)) * 4;
-      const int mb = (q / (kBK / 4)) * 8;
-      const bool ok = mb < cv;
+      for (int ks = 0; ks < 4; ++ks) {
+        const int c = (2 * ks + (lane >> 5)) ^ ((r >> 1) & 7);
+        base[ks] = (uint32_t)(r * kRowBytes + c * 16);
+      }
+    } else {
+      const int g = lane >> 4, s = lane & 15, j = s >> 2, q = s & 3;
+      const int k = 8 * (g >> 1) + j;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const uint32_t off = ok ? (uint32_t)((kb + rr) * ld + mb) * 2u : kOob;
-        r[i][rr] = buf_load16(rs, off);
+      for (int t = 0; t < TS; ++t) {
+        const int mn = row0 + 32 * t + 16 * (g & 1) + 4 * q;
+        const int c = (mn >> 3) ^ (4 * (k & 3));
+        base[t] = (uint32_t)(k * kRowBytes + c * 16 + (mn & 7) * 2);
       }
     }
   }
-  __device__ void store(uint16_t* s) const {
-#pragma unroll
-    for (int i = 0; i < kBlocks; ++i) {
-      const int q = threadIdx.x + i * kGemmThreads;
-      const int kb = (q % (kBK / 4)) * 4;
-      const int mb = (q / (kBK / 4)) * 8;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&r[i][0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&r[i][1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&r[i][2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&r[i][3]);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        // Element 2w: low halves; element 2w+1: high halves.
-        uint2 lo, hi;
-        lo.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u);
-        lo.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u);
-        hi.x = __builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u);
-        hi.y = __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u);
-        *reinterpret_cast<uint2*>(s + (mb + 2 * w) * kLdsStride + kb) = lo;
-        *reinterpret_cast<uint2*>(s + (mb + 2 * w + 1) * kLdsStride + kb) = hi;
-      }
+  template <typename V>
+  __device__ V read(const char* lds, int t, int ks) const {
+    if (KMAJ) {
+      return *reinterpret_cast<const V*>(lds + base[ks] + t * 32 * kRowBytes);
+    } else {
+      const char* p = lds + base[t] + 16 * ks * kRowBytes;
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+      const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * kRowBytes));
+      const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      return __builtin_bit_cast(V, v);
     }
   }
-};
-
-template <bool KCONTIG, int ROWS>
-struct LoaderSel;
-template <int ROWS>
-struct LoaderSel<true, ROWS> {
-  typedef LoaderK<ROWS> type;
-};
-template <int ROWS>
-struct LoaderSel<false, ROWS> {
-  typedef LoaderM<ROWS> type;
 };
 
 struct GemmArgs {
@@ -271,68 +305,51 @@ __device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int
   nt = (int)(rem / gsz);
 }
 
-// Persistent: one or two workgroups per CU loop over output tiles. Tiles are
-// dealt to XCDs in contiguous ranges (neighbouring tiles share operand panels
-// in that XCD's L2), and a tile's output stores drain while the next tile
-// computes. Each tile is BM x BN, computed by 4 waves (2 x 2); each wave owns a
-// (BM/2) x (BN/2) block of 32x32 MFMA tiles. The MFMA is issued with the B
-// fragment as its first operand, so each lane's accumulator holds 4
-// consecutive output columns of one output row (packable 8-byte groups).
-// K advances 64 per iteration through two LDS stages (one barrier per
-// iteration); the epilogue stages the bf16/fp16 tile through LDS and writes
-// 16-byte row chunks.
-template <typename T, int MODE, int BM, int BN>
-__global__ void __launch_bounds__(kGemmThreads)
-__attribute__((amdgpu_waves_per_eu(1, BM * BN >= 256 * 128 ? 1 : 2)))
+// One BM x BN output tile per workgroup of 8 waves (WGM x WGN grid, two
+// waves per SIMD); each wave owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA
+// tiles. The MFMA is issued with the B fragment as its first operand, so
+// each lane's accumulator holds 4 consecutive output columns of one output
+// row. K advances 64 per iteration through two LDS stages, one barrier per
+// iteration: the loads of stage kt+1 are issued right after the barrier and
+// land while stage kt is multiplied.
+template <typename T, int MODE, int BM, int BN, int WGM>
+__global__ void __launch_bounds__(kMfmaThreads)
 gg_mfma_kernel(GemmArgs g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WGN = kMfmaWaves / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int kStageA = BM * kLdsStride;
-  constexpr int kStage = (BM + BN) * kLdsStride;
-  constexpr int kEpiStride = BN + 8;
-  constexpr int kLdsElems = (2 * kStage > BM * kEpiStride) ? 2 * kStage : BM * kEpiStride;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[kLdsElems];
+  static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
+  constexpr bool kAK = MODE != kDw;   // A operand K-major?
+  constexpr bool kBKm = MODE == kDx;  // B operand K-major?
+  typedef OperandTile<BM, kAK> TA;
+  typedef OperandTile<BN, kBKm> TB;
+  constexpr int kStage = TA::kBytes + TB::kBytes;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
   __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
-
-  constexpr bool kAK = MODE != kDw;   // A operand K-contiguous?
-  constexpr bool kBK_ = MODE == kDx;  // B operand K-contiguous?
-  typedef typename LoaderSel<kAK, BM>::type LA;
-  typedef typename LoaderSel<kBK_, BN>::type LB;
 
   int64_t mtiles = g.mtiles;
   if (MODE != kDw) {
     build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
     mtiles = s_pref[g.E];
   }
-  const int64_t total = mtiles * g.ntn;
-  // Blocks are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8).
-  // XCD x owns a contiguous range of tiles, sized by how many blocks it has;
-  // its blocks walk that range in step. With one tile per block (large
-  // tiles, non-persistent launch) this reduces to a renumbering.
-  constexpr int kXcd = 8;
-  const int64_t G = gridDim.x;
-  const int xcd = blockIdx.x % kXcd;
-  const int64_t q = G / kXcd, r = G % kXcd;
-  const int64_t before = xcd * q + (xcd < r ? xcd : r);
-  const int64_t nbx = q + (xcd < r ? 1 : 0);
-  const int64_t t_end = total * (before + nbx) / G;
-  for (int64_t logical = total * before / G + blockIdx.x / kXcd; logical < t_end;
-       logical += nbx) {
+  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
+  if (logical >= mtiles * g.ntn) return;
+  int64_t mt;
+  int nt;
+  tile_coords(logical, mtiles, g.ntn, mt, nt);
+
   const uint16_t* pa;
   const uint16_t* pb;
   int64_t lda, ldb, rows_valid, cols_valid, kred;
   uint16_t* po;
   int64_t ldo;
-
-  int64_t mt;
-  int nt;
-  tile_coords(logical, mtiles, g.ntn, mt, nt);
-
   if (MODE == kDw) {
     const int e = (int)(mt / g.ntm);
     const int mtl = (int)(mt % g.ntm);
     int64_t r0, r1;
     expert_rows(g.offsets, e, g.A, r0, r1);
+    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
+    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
     kred = r1 - r0;
     pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * BM;
     lda = g.K;
@@ -347,6 +364,11 @@ gg_mfma_kernel(GemmArgs g) {
     int e;
     int64_t r0, r1, mtl;
     find_m_tile(g.offsets, g.E, g.A, s_pref, mt, e, r0, r1, mtl);
+    // Uniform across the workgroup (read from LDS / HBM): keep them scalar.
+    e = __builtin_amdgcn_readfirstlane(e);
+    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
+    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
+    mtl = (int64_t)__builtin_amdgcn_readfirstlane((int)mtl);
     const int64_t row0 = r0 + mtl * BM;
     rows_valid = r1 - row0;
     if (MODE == kFwd) {
@@ -371,8 +393,35 @@ gg_mfma_kernel(GemmArgs g) {
   }
 
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  TA ta;
+  TB tb;
+  ta.init(lda, wave, lane);
+  tb.init(ldb, wave, lane);
+  FragReader<BM, kAK, TM> fa;
+  FragReader<BN, kBKm, TN> fb;
+  fa.init(wm * WM, lane);
+  fb.init(wn * WN, lane);
+
+  const int64_t rv = rows_valid < BM ? rows_valid : BM;
+  const int64_t cv = cols_valid < BN ? cols_valid : BN;
+  // Readable bytes from a tile origin, given kv valid reduction elements.
+  auto range_a = [&](int64_t kv) {
+    return kAK ? ((rv - 1) * lda + kv) * 2 : ((kv - 1) * lda + rv) * 2;
+  };
+  auto range_b = [&](int64_t kv) {
+    return kBKm ? ((cv - 1) * ldb + kv) * 2 : ((kv - 1) * ldb + cv) * 2;
+  };
+  const int64_t a_kstep = kAK ? kBK : kBK * lda;
+  const int64_t b_kstep = kBKm ? kBK : kBK * ldb;
+  auto issue = [&](int64_t kt, char* la, char* lb) {
+    const int64_t kleft = kred - kt * kBK;
+    const int64_t kv = kleft < kBK ? kleft : kBK;
+    ta.issue(pa + kt * a_kstep, range_a(kv), la, kv, wave);
+    tb.issue(pb + kt * b_kstep, range_b(kv), lb, kv, wave);
+  };
 
   f32x16_t acc[TM][TN];
 #pragma unroll
@@ -382,107 +431,69 @@ gg_mfma_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  LA la;
-  LB lb;
-  const int64_t nk = ceil_div(kred, kBK);
-  // Operand pointers advance along the reduction dimension.
-  const int64_t a_kstep = kAK ? kBK : kBK * lda;
-  const int64_t b_kstep = kBK_ ? kBK : kBK * ldb;
-  if (nk > 0) {
-    la.load(pa, lda, rows_valid, kred);
-    lb.load(pb, ldb, cols_valid, kred);
-    la.store(smem);
-    lb.store(smem + kStageA);
-  }
-  __syncthreads();
   typedef typename mfma_op<T>::vec vec;
-  // Fragments for k-step ks+1 are read from LDS while the MFMAs of k-step
-  // ks run (two register sets), hiding LDS latency inside one wave.
-  auto compute = [&](const uint16_t* sa, const uint16_t* sb) {
-    const uint16_t* pa_l = sa + (wm * WM + (lane & 31)) * kLdsStride + (lane >> 5) * 8;
-    const uint16_t* pb_l = sb + (wn * WN + (lane & 31)) * kLdsStride + (lane >> 5) * 8;
+  // Fragments for substep ks+1 are read (into the other register set)
+  // before the MFMAs of ks are issued; scheduling fences keep that order, so
+  // the LDS latency of ks+1 hides behind the MFMAs of ks.
+  auto compute = [&](const char* sa, const char* sb) {
     vec av[2][TM], bv[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const vec*>(pa_l + i * 32 * kLdsStride);
+    for (int i = 0; i < TM; ++i) av[0][i] = fa.template read<vec>(sa, i, 0);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bv[0][j] = *reinterpret_cast<const vec*>(pb_l + j * 32 * kLdsStride);
+    for (int j = 0; j < TN; ++j) bv[0][j] = fb.template read<vec>(sb, j, 0);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int cur = ks & 1;
       if (ks + 1 < kBK / 16) {
-        const int kof = (ks + 1) * 16;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          av[cur ^ 1][i] = *reinterpret_cast<const vec*>(pa_l + i * 32 * kLdsStride + kof);
+        for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bv[cur ^ 1][j] = *reinterpret_cast<const vec*>(pb_l + j * 32 * kLdsStride + kof);
+        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = fb.template read<vec>(sb, j, ks + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma_op<T>::run(bv[cur][j], av[cur][i], acc[i][j]);
-      // Keep each k-step's reads ahead of its MFMAs, and the MFMAs of step
-      // ks ahead of the reads for step ks+2 (no reordering across).
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Steady state (branch-free body): load tile kt+1 into registers, compute
-  // tile kt from LDS, store tile kt+1 into the other LDS stage, one barrier.
-  for (int64_t kt = 0; kt + 1 < nk; ++kt) {
-    const int64_t kleft = kred - (kt + 1) * kBK;
-    // The next tile's buffer loads go out first; their latency is covered
-    // by this tile's MFMAs, and the LDS stores come after them.
-    la.load(pa + (kt + 1) * a_kstep, lda, rows_valid, kleft);
-    lb.load(pb + (kt + 1) * b_kstep, ldb, cols_valid, kleft);
-    __builtin_amdgcn_sched_barrier(0);
-    const uint16_t* sa = smem + (kt & 1) * kStage;
-    compute(sa, sa + kStageA);
-    uint16_t* nxt = smem + ((kt + 1) & 1) * kStage;
-    la.store(nxt);
-    lb.store(nxt + kStageA);
+  // Stage kt&1 is multiplied while stage (kt+1)&1 fills; the barrier at the
+  // top of each k-step publishes the landed stage and retires every wave's
+  // reads of the stage about to be refilled.
+  const int64_t nk = ceil_div(kred, kBK);
+  if (nk > 0) issue(0, smem, smem + TA::kBytes);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    wait_vmcnt0();
     __syncthreads();
+    char* nxt = smem + ((kt + 1) & 1) * kStage;
+    if (kt + 1 < nk) issue(kt + 1, nxt, nxt + TA::kBytes);
+    const char* cur = smem + (kt & 1) * kStage;
+    compute(cur, cur + TA::kBytes);
   }
-  if (nk > 0) {
-    const uint16_t* sa = smem + ((nk - 1) & 1) * kStage;
-    compute(sa, sa + kStageA);
-  }
-  __syncthreads();
 
-  // Epilogue. acc[i][j][v] = C[m][n] with m = wm*WM + 32i + lane%32 and
-  // n = wn*WN + 32j + 8*(v/4) + 4*(lane/32) + v%4: each lane packs 4
-  // consecutive columns into 8 bytes of the LDS staging tile.
+  // Epilogue: acc[i][j][v] = C[m][n] with m = wm*WM + 32i + lane%32 and
+  // n = wn*WN + 32j + 8*(v/4) + 4*(lane/32) + v%4; each lane stores 4
+  // consecutive columns (8 bytes) per group.
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    const int m = wm * WM + i * 32 + (lane & 31);
+    if (m >= rows_valid) continue;
+    uint16_t* prow = po + (int64_t)m * ldo;
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int m = wm * WM + i * 32 + (lane & 31);
         const int n = wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
+        if (n >= cols_valid) continue;
         uint2 pk;
         pk.x = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 0]) |
                ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 1]) << 16);
         pk.y = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 2]) |
                ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 3]) << 16);
-        *reinterpret_cast<uint2*>(smem + m * kEpiStride + n) = pk;
+        *reinterpret_cast<uint2*>(prow + n) = pk;
       }
-  __syncthreads();
-  constexpr int kChunksPerRow = BN / 8;
-#pragma unroll 4
-  for (int q = threadIdx.x; q < BM * kChunksPerRow; q += kGemmThreads) {
-    const int row = q / kChunksPerRow;
-    const int c = (q % kChunksPerRow) * 8;
-    if (row < rows_valid && c < cols_valid)
-      *reinterpret_cast<uint4*>(po + (int64_t)row * ldo + c) =
-          *reinterpret_cast<const uint4*>(smem + row * kEpiStride + c);
-  }
-  __syncthreads();  // the staging tile is read before the next tile reuses LDS
-  // 256x256 tiles are launched one per workgroup: a single pass, so nothing
-  // is carried (or hoisted) across tiles.
-  if constexpr (BM * BN >= 256 * 256) break;
   }
 }
 
@@ -632,7 +643,7 @@ int device_cus() {
   return cache[dev];
 }
 
-template <int MODE, int BM, int BN>
+template <int MODE, int BM, int BN, int WGM>
 int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   g.ntn = (int32_t)ceil_div(out_cols, BN);
   if (MODE == kDw) {
@@ -645,18 +656,13 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t tiles = g.mtiles * g.ntn;
   if (tiles == 0) return NT_OK;
   if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
-  // 256x256 tiles: one tile per workgroup (a tile loop would push the
-  // 512-register kernel into spills); smaller tiles: persistent workgroups,
-  // one (256x128) or two (128x128) per CU.
-  const int per_cu = BM * BN >= 256 * 128 ? 1 : 2;
-  const int64_t nblocks = BM * BN >= 256 * 256
-                              ? tiles
-                              : std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
-  const dim3 grid((unsigned)nblocks);
+  const dim3 grid((unsigned)tiles);
   if (dtype == NT_BF16)
-    hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE, BM, BN>), grid, dim3(kGemmThreads), 0, s, g);
+    hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE, BM, BN, WGM>), grid, dim3(kMfmaThreads), 0, s,
+                       g);
   else
-    hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE, BM, BN>), grid, dim3(kGemmThreads), 0, s, g);
+    hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE, BM, BN, WGM>), grid, dim3(kMfmaThreads), 0, s,
+                       g);
   return launch_status();
 }
 
@@ -666,9 +672,9 @@ template <int MODE>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t rows = MODE == kDw ? g.K * g.E : g.A;
   auto tiles = [&](int bm, int bn) { return ceil_div(rows, bm) * ceil_div(out_cols, bn); };
-  if (tiles(256, 256) >= 1024) return launch_mfma<MODE, 256, 256>(dtype, g, out_cols, s);
-  if (tiles(256, 128) >= 768) return launch_mfma<MODE, 256, 128>(dtype, g, out_cols, s);
-  return launch_mfma<MODE, 128, 128>(dtype, g, out_cols, s);
+  if (tiles(256, 256) >= 1024) return launch_mfma<MODE, 256, 256, 2>(dtype, g, out_cols, s);
+  if (tiles(256, 128) >= 768) return launch_mfma<MODE, 256, 128, 4>(dtype, g, out_cols, s);
+  return launch_mfma<MODE, 128, 128, 4>(dtype, g, out_cols, s);
 }
 
 template <int MODE>
