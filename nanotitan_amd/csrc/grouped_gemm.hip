@@ -119,7 +119,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;            // reduction elements per k-step
 constexpr int kMfmaThreads = 512;  // 8 waves, two per SIMD
 constexpr int kMfmaWaves = kMfmaThreads / kWave;
 
@@ -163,14 +162,22 @@ __device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t voff, uint3
       : "memory", "m0");
 }
 
-__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N of this wave's vector-memory loads are in flight
+// (they retire in issue order, so the older ones are complete).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
-// One operand tile in LDS, ROWS (m or n) x kBK (reduction) 16-bit elements.
+// One operand tile in LDS, ROWS (m or n) x BK (reduction, 64 or 32) 16-bit
+// elements.
 //
 // K-major (the reduction index is contiguous in HBM): row r of the tile is
-// kBK elements = 128 B = 8 chunks of 16 B, chunk c stored at position
-// c ^ ((r >> 1) & 7). An MFMA fragment read (ds_read_b128, 16 lanes per LDS
-// cycle: rows r..r+15, one chunk) then touches all 64 banks once.
+// BK elements = CPR chunks of 16 B; RPW = 16 / CPR rows share one 256-byte
+// sweep of the 64 banks. Chunk c of row r is stored at c ^ ((r / RPW) % CPR).
+// An MFMA fragment read (ds_read_b128, 16 lanes per LDS cycle: rows
+// r..r+15, one chunk) then touches all 64 banks once.
 //
 // MN-major (m / n contiguous in HBM): row k of the tile holds ROWS elements
 // (ROWS/8 chunks), chunk c stored at c ^ (4 * (k & 3)). Fragments come from
@@ -184,34 +191,29 @@ __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)
 // Wave w issues instructions w, w+8, ...; for a given lane these differ only
 // by a whole number of XOR periods, so one per-lane offset plus a uniform
 // stride per instruction covers them.
-template <int ROWS, bool KMAJ>
+template <int ROWS, bool KMAJ, int BK, int NW>
 struct OperandTile {
-  static constexpr int kBytes = ROWS * kBK * 2;
+  static_assert(BK == 32 || BK == 64, "k-step of 32 or 64 elements");
+  static constexpr int kBytes = ROWS * BK * 2;
   static constexpr int kInsts = kBytes / 1024;   // 1 KiB per load instruction
-  static constexpr int kPer = kInsts / kMfmaWaves;
-  static_assert(kPer >= 1 && kInsts % kMfmaWaves == 0, "tile too small for 8 waves");
+  static constexpr int kPer = kInsts / NW;
+  static_assert(kPer >= 1 && kInsts % NW == 0, "tile too small for the wave count");
   static_assert(KMAJ || ROWS >= 128, "MN-major tiles need at least 16 chunks per row");
-  static constexpr int kRowBytes = KMAJ ? kBK * 2 : ROWS * 2;
+  static constexpr int kRowBytes = KMAJ ? BK * 2 : ROWS * 2;
   static constexpr int kRowsPerInst = 1024 / kRowBytes;
+  static constexpr int kCpr = KMAJ ? BK / 8 : ROWS / 8;  // chunks per row
+  static constexpr int kRpw = 16 / (BK / 8);             // K-major rows per bank sweep
 
   uint32_t off;     // byte offset of this lane's chunk (instruction `wave`) from the tile origin
   uint32_t kchunk;  // K-major: first reduction index of the lane's chunk
   uint32_t ustep;   // byte stride between this wave's successive instructions
 
   __device__ void init(int64_t ld, int wave, int lane) {
-    const int t = wave;
-    int r, c;
-    if (KMAJ) {
-      r = 8 * t + (lane >> 3);
-      c = (lane & 7) ^ ((r >> 1) & 7);
-    } else {
-      constexpr int kCpr = ROWS / 8;  // chunks per row
-      r = kRowsPerInst * t + lane / kCpr;
-      c = (lane % kCpr) ^ (4 * (r & 3));
-    }
+    const int r = kRowsPerInst * wave + lane / kCpr;
+    const int c = KMAJ ? (lane % kCpr) ^ ((r / kRpw) % kCpr) : (lane % kCpr) ^ (4 * (r & 3));
     off = (uint32_t)((int64_t)r * ld + c * 8) * 2u;
     kchunk = (uint32_t)(c * 8);
-    ustep = (uint32_t)(kMfmaWaves * kRowsPerInst * ld * 2);
+    ustep = (uint32_t)(NW * kRowsPerInst * ld * 2);
   }
 
   // Issue this wave's share of the tile's loads. `base` is the tile origin
@@ -222,26 +224,29 @@ struct OperandTile {
     const i32x4_t rs = make_rsrc(base, range);
     const uint32_t l0 = lds_addr(lds) + (uint32_t)wave * 1024u;
     uint32_t v = off;
-    if (KMAJ && kv < kBK && (int64_t)kchunk >= kv) v = kOob;
+    if (KMAJ && kv < BK && (int64_t)kchunk >= kv) v = kOob;
 #pragma unroll
     for (int u = 0; u < kPer; ++u)
-      load16_to_lds(rs, v + (uint32_t)u * ustep, l0 + (uint32_t)(u * kMfmaWaves * 1024));
+      load16_to_lds(rs, v + (uint32_t)u * ustep,
+                    __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
   }
 };
 
 // Per-lane LDS byte offsets of the fragment reads of one operand: TS 32-row
-// sub-tiles starting at row `row0` of the tile, for each of the 4 k-substeps
-// of 16 elements.
-template <int ROWS, bool KMAJ, int TS>
+// sub-tiles starting at row `row0` of the tile, for each of the BK/16
+// k-substeps of 16 elements.
+template <int ROWS, bool KMAJ, int TS, int BK>
 struct FragReader {
-  static constexpr int kRowBytes = KMAJ ? kBK * 2 : ROWS * 2;
-  uint32_t base[KMAJ ? 4 : TS];
+  static constexpr int kRowBytes = KMAJ ? BK * 2 : ROWS * 2;
+  static constexpr int kCpr = BK / 8;
+  static constexpr int kRpw = 16 / kCpr;
+  uint32_t base[KMAJ ? BK / 16 : TS];
   __device__ void init(int row0, int lane) {
     if (KMAJ) {
       const int r = row0 + (lane & 31);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int c = (2 * ks + (lane >> 5)) ^ ((r >> 1) & 7);
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int c = (2 * ks + (lane >> 5)) ^ ((r / kRpw) % kCpr);
         base[ks] = (uint32_t)(r * kRowBytes + c * 16);
       }
     } else {
@@ -281,16 +286,6 @@ struct GemmArgs {
   int64_t mtiles;   // m-tile slots enumerated by the grid (upper bound for fwd / dX)
 };
 
-// Workgroup ids are dealt to the 8 XCDs round-robin; renumber them so each
-// XCD receives a contiguous range of logical tiles (tiles that share operand
-// panels then share that XCD's L2).
-__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t G) {
-  constexpr int kXcd = 8;
-  const int64_t q = G / kXcd, r = G % kXcd;
-  const int64_t x = bid % kXcd, s = bid / kXcd;
-  return x * q + (x < r ? x : r) + s;
-}
-
 // Logical tile -> (m-tile, n-tile): groups of kGroupM m-tiles, m fastest
 // inside a group, so neighbouring logical tiles reuse both A and B panels.
 constexpr int kGroupM = 8;
@@ -305,26 +300,214 @@ __device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int
   nt = (int)(rem / gsz);
 }
 
-// One BM x BN output tile per workgroup of 8 waves (WGM x WGN grid, two
-// waves per SIMD); each wave owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA
-// tiles. The MFMA is issued with the B fragment as its first operand, so
-// each lane's accumulator holds 4 consecutive output columns of one output
-// row. K advances 64 per iteration through two LDS stages, one barrier per
-// iteration: the loads of stage kt+1 are issued right after the barrier and
-// land while stage kt is multiplied.
-template <typename T, int MODE, int BM, int BN, int WGM>
-__global__ void __launch_bounds__(kMfmaThreads)
+// Operand pointers, strides and valid extents of one output tile.
+struct TileJob {
+  const uint16_t* pa;  // A operand origin (tile rows, reduction 0)
+  const uint16_t* pb;  // B operand origin (tile columns, reduction 0)
+  int64_t lda, ldb;
+  int64_t rows_valid, cols_valid;  // output rows / columns from the tile origin
+  int64_t kred;                    // reduction length
+  uint16_t* po;
+  int64_t ldo;
+};
+
+// Operands and extents of logical output tile `logical` (< mtiles * ntn).
+// For the row-tiled modes s_pref must hold the m-tile prefix of the experts
+// (build_m_prefix) and `mtiles` its total.
+template <int MODE, int BM, int BN>
+__device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pref, int64_t mtiles,
+                                          int64_t logical, TileJob& j) {
+  int64_t mt;
+  int nt;
+  tile_coords(logical, mtiles, g.ntn, mt, nt);
+  if (MODE == kDw) {
+    const int e = (int)(mt / g.ntm);
+    const int mtl = (int)(mt % g.ntm);
+    int64_t r0, r1;
+    expert_rows(g.offsets, e, g.A, r0, r1);
+    // Uniform across the workgroup (read from HBM / LDS): keep them scalar.
+    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
+    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
+    j.kred = r1 - r0;
+    j.pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * BM;
+    j.lda = g.K;
+    j.pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * BN;
+    j.ldb = g.N;
+    j.rows_valid = g.K - (int64_t)mtl * BM;
+    j.cols_valid = g.N - (int64_t)nt * BN;
+    j.po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * BM * g.N +
+           (int64_t)nt * BN;
+    j.ldo = g.N;
+  } else {
+    int e;
+    int64_t r0, r1, mtl;
+    find_m_tile(g.offsets, g.E, g.A, s_pref, mt, e, r0, r1, mtl);
+    e = __builtin_amdgcn_readfirstlane(e);
+    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
+    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
+    mtl = (int64_t)__builtin_amdgcn_readfirstlane((int)mtl);
+    const int64_t row0 = r0 + mtl * BM;
+    j.rows_valid = r1 - row0;
+    if (MODE == kFwd) {
+      j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
+      j.lda = g.K;
+      j.pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN;
+      j.ldb = g.N;
+      j.cols_valid = g.N - (int64_t)nt * BN;
+      j.kred = g.K;
+      j.po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * BN;
+      j.ldo = g.N;
+    } else {  // kDx
+      j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
+      j.lda = g.N;
+      j.pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
+      j.ldb = g.N;
+      j.cols_valid = g.K - (int64_t)nt * BN;
+      j.kred = g.N;
+      j.po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * BN;
+      j.ldo = g.K;
+    }
+  }
+}
+
+// Global loads of one k-step of both operands of a tile into an LDS stage.
+template <int BM, int BN, bool AK, bool BKM, int BK, int NW>
+struct StageLoader {
+  typedef OperandTile<BM, AK, BK, NW> TA;
+  typedef OperandTile<BN, BKM, BK, NW> TB;
+  TA ta;
+  TB tb;
+  const uint16_t* pa;
+  const uint16_t* pb;
+  int64_t lda, ldb, rv, cv, kred;
+  int wave;
+  __device__ void init(const TileJob& j, int wave_, int lane) {
+    pa = j.pa;
+    pb = j.pb;
+    lda = j.lda;
+    ldb = j.ldb;
+    rv = j.rows_valid < BM ? j.rows_valid : BM;
+    cv = j.cols_valid < BN ? j.cols_valid : BN;
+    kred = j.kred;
+    wave = wave_;
+    ta.init(lda, wave, lane);
+    tb.init(ldb, wave, lane);
+  }
+  // Issue this wave's loads of k-step kt into the stage at `lds` (A tile
+  // first, then the B tile).
+  __device__ void issue(int64_t kt, char* lds) const {
+    const int64_t kleft = kred - kt * BK;
+    const int64_t kv = kleft < BK ? kleft : BK;
+    // Readable bytes from each tile origin: up to the last valid element.
+    const int64_t ra = AK ? ((rv - 1) * lda + kv) * 2 : ((kv - 1) * lda + rv) * 2;
+    const int64_t rb = BKM ? ((cv - 1) * ldb + kv) * 2 : ((kv - 1) * ldb + cv) * 2;
+    ta.issue(pa + kt * (AK ? BK : BK * lda), ra, lds, kv, wave);
+    tb.issue(pb + kt * (BKM ? BK : BK * ldb), rb, lds + TA::kBytes, kv, wave);
+  }
+};
+
+// Epilogue: acc[i][j][v] = C[m][n] with m = m0 + 32i + lane%32 and
+// n = n0 + 32j + 8*(v/4) + 4*(lane/32) + v%4; each lane stores 4
+// consecutive columns (8 bytes) per group, rounded once (RNE).
+template <typename T, int TM, int TN>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[TM][TN], const TileJob& j, int m0,
+                                           int n0, int lane) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + i * 32 + (lane & 31);
+    if (m >= j.rows_valid) continue;
+    uint16_t* prow = j.po + (int64_t)m * j.ldo;
+#pragma unroll
+    for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int n = n0 + jn * 32 + 8 * gq + 4 * (lane >> 5);
+        if (n >= j.cols_valid) continue;
+        uint2 pk;
+        pk.x = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 0]) |
+               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 1]) << 16);
+        pk.y = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 2]) |
+               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 3]) << 16);
+        *reinterpret_cast<uint2*>(prow + n) = pk;
+      }
+  }
+}
+
+// Epilogue through LDS for 64-column wave blocks: each 32-row sub-tile is
+// rounded (RNE), written to this wave's LDS scratch (32 rows, 136-byte
+// pitch: the 8-byte writes of 32 rows fall on distinct banks), and read back
+// 16 bytes per lane so that every store instruction writes 8 whole
+// 128-byte row segments. `scratch` is 32 * 136 bytes private to the wave;
+// LDS operations of one wave complete in order, so no barrier is needed.
+constexpr int kEpiPitch = 136;
+constexpr int kEpiBytes = 32 * kEpiPitch;
+template <typename T, int TM, int TN>
+__device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+                                               int m0, int n0, int lane, char* scratch) {
+  static_assert(TN == 2, "64-column wave blocks");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
+        uint2 pk;
+        pk.x = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 0]) |
+               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 1]) << 16);
+        pk.y = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 2]) |
+               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 3]) << 16);
+        *reinterpret_cast<uint2*>(scratch + (lane & 31) * kEpiPitch + c * 2) = pk;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rr = q * 8 + (lane >> 3);
+      const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kEpiPitch + (lane & 7) * 16);
+      const int m = m0 + i * 32 + rr;
+      const int n = n0 + (lane & 7) * 8;
+      if (m < j.rows_valid && n < j.cols_valid)
+        *reinterpret_cast<uint4*>(j.po + (int64_t)m * j.ldo + n) = v;
+    }
+  }
+}
+
+template <typename T, int TM, int TN>
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[TM][TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+}
+
+// Persistent grouped GEMM. Each workgroup of WGM x WGN waves walks a range
+// of BM x BN output tiles; each wave owns a (BM/WGM) x (BN/WGN) block of
+// 32x32 MFMA tiles. The MFMA is issued with the B fragment as its first
+// operand, so each lane's accumulator holds 4 consecutive output columns of
+// one output row. K advances BK per iteration through a ring of NS LDS
+// stages: the loads of stage kt+NS-1 are issued right after the barrier of
+// iteration kt and have NS-1 iterations of MFMAs to land. The first stages
+// of a workgroup's next tile are issued before the current tile's results
+// are stored, so their latency hides behind the epilogue.
+//
+// Tiles are dealt to XCDs in contiguous ranges (workgroup b runs on XCD
+// b % 8), so tiles that share operand panels share that XCD's L2; inside a
+// range, tile_coords walks groups of kGroupM m-tiles with m fastest.
+template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS>
+__global__ void __launch_bounds__(WGM * WGN * kWave)
 gg_mfma_kernel(GemmArgs g) {
-  constexpr int WGN = kMfmaWaves / WGM;
+  constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
+  static_assert(NS >= 2, "at least two LDS stages");
   constexpr bool kAK = MODE != kDw;   // A operand K-major?
   constexpr bool kBKm = MODE == kDx;  // B operand K-major?
-  typedef OperandTile<BM, kAK> TA;
-  typedef OperandTile<BN, kBKm> TB;
-  constexpr int kStage = TA::kBytes + TB::kBytes;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW> Loader;
+  constexpr int kStage = Loader::TA::kBytes + Loader::TB::kBytes;
+  constexpr int kLoadsPerStage = Loader::TA::kPer + Loader::TB::kPer;  // per wave
+  __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
   __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
 
   int64_t mtiles = g.mtiles;
@@ -332,106 +515,36 @@ gg_mfma_kernel(GemmArgs g) {
     build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
     mtiles = s_pref[g.E];
   }
-  const int64_t logical = xcd_remap(blockIdx.x, gridDim.x);
-  if (logical >= mtiles * g.ntn) return;
-  int64_t mt;
-  int nt;
-  tile_coords(logical, mtiles, g.ntn, mt, nt);
-
-  const uint16_t* pa;
-  const uint16_t* pb;
-  int64_t lda, ldb, rows_valid, cols_valid, kred;
-  uint16_t* po;
-  int64_t ldo;
-  if (MODE == kDw) {
-    const int e = (int)(mt / g.ntm);
-    const int mtl = (int)(mt % g.ntm);
-    int64_t r0, r1;
-    expert_rows(g.offsets, e, g.A, r0, r1);
-    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
-    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
-    kred = r1 - r0;
-    pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * BM;
-    lda = g.K;
-    pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * BN;
-    ldb = g.N;
-    rows_valid = g.K - (int64_t)mtl * BM;
-    cols_valid = g.N - (int64_t)nt * BN;
-    po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * BM * g.N +
-         (int64_t)nt * BN;
-    ldo = g.N;
-  } else {
-    int e;
-    int64_t r0, r1, mtl;
-    find_m_tile(g.offsets, g.E, g.A, s_pref, mt, e, r0, r1, mtl);
-    // Uniform across the workgroup (read from LDS / HBM): keep them scalar.
-    e = __builtin_amdgcn_readfirstlane(e);
-    r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
-    r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
-    mtl = (int64_t)__builtin_amdgcn_readfirstlane((int)mtl);
-    const int64_t row0 = r0 + mtl * BM;
-    rows_valid = r1 - row0;
-    if (MODE == kFwd) {
-      pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
-      lda = g.K;
-      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN;
-      ldb = g.N;
-      cols_valid = g.N - (int64_t)nt * BN;
-      kred = g.K;
-      po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * BN;
-      ldo = g.N;
-    } else {  // kDx
-      pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
-      lda = g.N;
-      pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
-      ldb = g.N;
-      cols_valid = g.K - (int64_t)nt * BN;
-      kred = g.N;
-      po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * BN;
-      ldo = g.K;
-    }
-  }
+  const int64_t total = mtiles * g.ntn;
+  constexpr int kXcd = 8;
+  const int64_t G = gridDim.x;
+  const int xcd = blockIdx.x % kXcd;
+  const int64_t q = G / kXcd, r = G % kXcd;
+  const int64_t before = xcd * q + (xcd < r ? xcd : r);
+  const int64_t nbx = q + (xcd < r ? 1 : 0);  // workgroups on this XCD
+  const int64_t t_end = total * (before + nbx) / G;
+  int64_t logical = total * before / G + blockIdx.x / kXcd;
+  if (logical >= t_end) return;
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wm = wave / WGN, wn = wave % WGN;
-
-  TA ta;
-  TB tb;
-  ta.init(lda, wave, lane);
-  tb.init(ldb, wave, lane);
-  FragReader<BM, kAK, TM> fa;
-  FragReader<BN, kBKm, TN> fb;
+  FragReader<BM, kAK, TM, BK> fa;
+  FragReader<BN, kBKm, TN, BK> fb;
   fa.init(wm * WM, lane);
   fb.init(wn * WN, lane);
 
-  const int64_t rv = rows_valid < BM ? rows_valid : BM;
-  const int64_t cv = cols_valid < BN ? cols_valid : BN;
-  // Readable bytes from a tile origin, given kv valid reduction elements.
-  auto range_a = [&](int64_t kv) {
-    return kAK ? ((rv - 1) * lda + kv) * 2 : ((kv - 1) * lda + rv) * 2;
-  };
-  auto range_b = [&](int64_t kv) {
-    return kBKm ? ((cv - 1) * ldb + kv) * 2 : ((kv - 1) * ldb + cv) * 2;
-  };
-  const int64_t a_kstep = kAK ? kBK : kBK * lda;
-  const int64_t b_kstep = kBKm ? kBK : kBK * ldb;
-  auto issue = [&](int64_t kt, char* la, char* lb) {
-    const int64_t kleft = kred - kt * kBK;
-    const int64_t kv = kleft < kBK ? kleft : kBK;
-    ta.issue(pa + kt * a_kstep, range_a(kv), la, kv, wave);
-    tb.issue(pb + kt * b_kstep, range_b(kv), lb, kv, wave);
-  };
-
-  f32x16_t acc[TM][TN];
+  TileJob job;
+  setup_job<MODE, BM, BN>(g, s_pref, mtiles, logical, job);
+  Loader ld;
+  ld.init(job, wave, lane);
+  int64_t nk = ceil_div(job.kred, BK);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  for (int s0 = 0; s0 < NS - 1; ++s0)
+    if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
 
   typedef typename mfma_op<T>::vec vec;
+  f32x16_t acc[TM][TN];
   // Fragments for substep ks+1 are read (into the other register set)
   // before the MFMAs of ks are issued; scheduling fences keep that order, so
   // the LDS latency of ks+1 hides behind the MFMAs of ks.
@@ -442,9 +555,9 @@ gg_mfma_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) bv[0][j] = fb.template read<vec>(sb, j, 0);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
+    for (int ks = 0; ks < BK / 16; ++ks) {
       const int cur = ks & 1;
-      if (ks + 1 < kBK / 16) {
+      if (ks + 1 < BK / 16) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
 #pragma unroll
@@ -459,41 +572,60 @@ gg_mfma_kernel(GemmArgs g) {
     }
   };
 
-  // Stage kt&1 is multiplied while stage (kt+1)&1 fills; the barrier at the
-  // top of each k-step publishes the landed stage and retires every wave's
-  // reads of the stage about to be refilled.
-  const int64_t nk = ceil_div(kred, kBK);
-  if (nk > 0) issue(0, smem, smem + TA::kBytes);
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    wait_vmcnt0();
-    __syncthreads();
-    char* nxt = smem + ((kt + 1) & 1) * kStage;
-    if (kt + 1 < nk) issue(kt + 1, nxt, nxt + TA::kBytes);
-    const char* cur = smem + (kt & 1) * kStage;
-    compute(cur, cur + TA::kBytes);
-  }
-
-  // Epilogue: acc[i][j][v] = C[m][n] with m = wm*WM + 32i + lane%32 and
-  // n = wn*WN + 32j + 8*(v/4) + 4*(lane/32) + v%4; each lane stores 4
-  // consecutive columns (8 bytes) per group.
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = wm * WM + i * 32 + (lane & 31);
-    if (m >= rows_valid) continue;
-    uint16_t* prow = po + (int64_t)m * ldo;
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
-        if (n >= cols_valid) continue;
-        uint2 pk;
-        pk.x = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 0]) |
-               ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 1]) << 16);
-        pk.y = (uint32_t)elem<T>::store(acc[i][j][4 * gq + 2]) |
-               ((uint32_t)elem<T>::store(acc[i][j][4 * gq + 3]) << 16);
-        *reinterpret_cast<uint2*>(prow + n) = pk;
+  while (true) {
+    zero_acc<T>(acc);
+    // Ring pipeline. Iteration kt waits until its own stage has landed (the
+    // loads of up to NS-2 younger stages may stay in flight: vector memory
+    // operations retire in issue order), and the barrier then publishes the
+    // stage to every wave and retires every wave's reads of the slot that
+    // is refilled next.
+    int slot = 0;
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int64_t younger = nk - 1 - kt;  // stages issued after this one (capped below)
+      if (younger >= NS - 2) {
+        wait_vmcnt<(NS - 2) * kLoadsPerStage>();
+      } else if (NS > 3 && younger == 2) {
+        wait_vmcnt<(NS > 3 ? 2 : 0) * kLoadsPerStage>();
+      } else if (NS > 2 && younger == 1) {
+        wait_vmcnt<(NS > 2 ? 1 : 0) * kLoadsPerStage>();
+      } else {
+        wait_vmcnt<0>();
       }
+      __syncthreads();
+      if (kt + NS - 1 < nk) {
+        int fill = slot + NS - 1;
+        if (fill >= NS) fill -= NS;
+        ld.issue(kt + NS - 1, smem + fill * kStage);
+      }
+      const char* cur = smem + slot * kStage;
+      compute(cur, cur + Loader::TA::kBytes);
+      slot = slot + 1 == NS ? 0 : slot + 1;
+    }
+    // Every wave is done with the stages; start the next tile's loads, then
+    // store this tile.
+    const int64_t next = logical + nbx;
+    const bool more = next < t_end;
+    __syncthreads();
+    TileJob nj;
+    if (more) {
+      setup_job<MODE, BM, BN>(g, s_pref, mtiles, next, nj);
+      ld.init(nj, wave, lane);
+      nk = ceil_div(nj.kred, BK);
+#pragma unroll
+      for (int s0 = 0; s0 < NS - 1; ++s0)
+        if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
+    }
+    if (TN == 2) {
+      // The ring's last slot is idle until the next tile's first iteration.
+      static_assert(NW * kEpiBytes <= kStage, "epilogue scratch fits one stage");
+      store_tile_lds<T>(acc, job, wm * WM, wn * WN, lane,
+                        smem + (NS - 1) * kStage + wave * kEpiBytes);
+    } else {
+      store_tile<T>(acc, job, wm * WM, wn * WN, lane);
+    }
+    if (!more) break;
+    job = nj;
+    logical = next;
   }
 }
 
@@ -643,38 +775,60 @@ int device_cus() {
   return cache[dev];
 }
 
-template <int MODE, int BM, int BN, int WGM>
-int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
+// Tile bookkeeping shared by the launchers: n-tiles, m-tile slots and the
+// grid size (one workgroup per tile).
+template <int MODE>
+int64_t plan_tiles(GemmArgs& g, int64_t out_cols, int BM, int BN) {
   g.ntn = (int32_t)ceil_div(out_cols, BN);
   if (MODE == kDw) {
     g.ntm = (int32_t)ceil_div(g.K, BM);
     g.mtiles = (int64_t)g.E * g.ntm;
   } else {
     g.ntm = 0;
-    g.mtiles = ceil_div(g.A, BM) + g.E;
+    g.mtiles = ceil_div(g.A, BM) + g.E;  // upper bound: each expert's last tile may be partial
   }
-  const int64_t tiles = g.mtiles * g.ntn;
+  return g.mtiles * g.ntn;
+}
+
+// Workgroups of `kernel` that fit on one CU at once.
+template <typename K>
+int blocks_per_cu(K kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1)
+    n = 1;
+  return n;
+}
+
+template <int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS>
+int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
+  const int64_t tiles = plan_tiles<MODE>(g, out_cols, BM, BN);
   if (tiles == 0) return NT_OK;
   if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
-  const dim3 grid((unsigned)tiles);
+  constexpr int threads = WGM * WGN * kWave;
+  auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS>;
+  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS>;
+  // Occupancy of this instantiation (bf16 and fp16 share resource usage).
+  static const int per_cu = blocks_per_cu(kb, threads);
+  // Persistent: at most one resident wave of workgroups; each walks tiles.
+  const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
+  const dim3 grid((unsigned)nblocks);
   if (dtype == NT_BF16)
-    hipLaunchKernelGGL((gg_mfma_kernel<bf16, MODE, BM, BN, WGM>), grid, dim3(kMfmaThreads), 0, s,
-                       g);
+    hipLaunchKernelGGL(kb, grid, dim3(threads), 0, s, g);
   else
-    hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE, BM, BN, WGM>), grid, dim3(kMfmaThreads), 0, s,
-                       g);
+    hipLaunchKernelGGL(kh, grid, dim3(threads), 0, s, g);
   return launch_status();
 }
 
-// Tile shape: 256x256 when the problem has enough tiles to fill the 256 CUs
-// a few times over, otherwise smaller tiles for more parallelism.
+// Tile shape (measured on MI355X over the configs' shapes): 256x256 with 8
+// waves unless that leaves fewer than 1.5 tiles per CU, then 128x128 with 4
+// waves (two workgroups per CU).
 template <int MODE>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t rows = MODE == kDw ? g.K * g.E : g.A;
-  auto tiles = [&](int bm, int bn) { return ceil_div(rows, bm) * ceil_div(out_cols, bn); };
-  if (tiles(256, 256) >= 1024) return launch_mfma<MODE, 256, 256, 2>(dtype, g, out_cols, s);
-  if (tiles(256, 128) >= 768) return launch_mfma<MODE, 256, 128, 4>(dtype, g, out_cols, s);
-  return launch_mfma<MODE, 128, 128, 4>(dtype, g, out_cols, s);
+  const int64_t tiles256 = ceil_div(rows, 256) * ceil_div(out_cols, 256);
+  if (tiles256 * 2 >= (int64_t)device_cus() * 3)
+    return launch_mfma<MODE, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
+  return launch_mfma<MODE, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
 }
 
 template <int MODE>
