@@ -2,8 +2,9 @@
 
 A step is one pass of the hot path over one batch: from router logits,
 fp32 softmax / stable top-k / renorm, fused count + offsets + pack, grouped
-GEMM up, GELU, grouped GEMM down, combine (activation dtype out), then the
-full backward to dX, dlogits, dW_up and dW_down. Inputs are resident in HBM
+GEMM up with the GELU in its epilogue, grouped GEMM down, combine
+(activation dtype out), then the full backward to dX, dlogits, dW_up and
+dW_down (the GELU backward fused into the down projection's dX GEMM). Inputs are resident in HBM
 before the timed region. Default workload: config C2 (30720 tokens, d=512,
 E=8, top-2, FFN 512->2048->512, bf16), synthetic seeded data, random-init
 weights.
@@ -79,7 +80,9 @@ class LaunchTimer:
 
     FAMILIES = {
         "grouped_gemm_kernel": "gemm",
+        "grouped_gemm_gelu": "gemm",
         "bwd_grouped_gemm_dX_kernel": "gemm",
+        "bwd_grouped_gemm_dX_gelu": "gemm",
         "bwd_grouped_gemm_dW_kernel": "gemm",
         "dispatch_tokens": "dispatch",
         "combine_inv": "combine_fwd",
@@ -114,11 +117,11 @@ class LaunchTimer:
     @staticmethod
     def _work(name, args):
         """Algorithmic work of one launch: FLOPs for GEMMs, bytes otherwise."""
-        if name == "grouped_gemm_kernel":
+        if name in ("grouped_gemm_kernel", "grouped_gemm_gelu"):
             X, _off, W = args
             return 2.0 * X.shape[0] * X.shape[1] * W.shape[2]
-        if name == "bwd_grouped_gemm_dX_kernel":
-            W, _off, G = args
+        if name in ("bwd_grouped_gemm_dX_kernel", "bwd_grouped_gemm_dX_gelu"):
+            W, _off, G = args[:3]
             return 2.0 * G.shape[0] * W.shape[1] * W.shape[2]
         if name == "bwd_grouped_gemm_dW_kernel":
             X, _off, G = args
@@ -169,16 +172,17 @@ def gpu_step(wl, W_up, W_down, ffn):
 
 
 class _GeluFFN(torch.nn.Module):
+    """Up -> GELU -> down experts on the fused grouped GEMMs (the layer's GeluExpertFFN)."""
+
     def __init__(self, W_up, W_down):
         super().__init__()
         self.W_up = W_up
         self.W_down = W_down
 
     def forward(self, packed_X, offsets):
-        from nanotitan_amd.moe_ops import grouped_gemm_fn
+        from nanotitan_amd.moe_ops import grouped_gelu_ffn_fn
 
-        h = torch.nn.functional.gelu(grouped_gemm_fn(packed_X, self.W_up, offsets))
-        return grouped_gemm_fn(h, self.W_down, offsets)
+        return grouped_gelu_ffn_fn(packed_X, self.W_up, self.W_down, offsets)
 
 
 def cpu_model() -> str:

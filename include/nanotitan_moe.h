@@ -179,7 +179,8 @@ int nt_route_topk_backward(const float* gates, const int32_t* topk, const float*
 
 /* ------------------------------------------------------------- grouped GEMM */
 
-/* Workspace for the grouped GEMMs (dW split-K partials and tile schedule). */
+/* Workspace for the grouped GEMMs: none is needed today (returns 0); kept so
+ * callers size it through one query if a later version needs one. */
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N);
 
 /* out[a,:] = X[a,:] @ W[e] for a in [offsets[e], offsets[e+1]), float32
@@ -196,9 +197,30 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dX, void* ws,
                        size_t ws_bytes, hipStream_t stream);
 
+/* Up-projection with the GELU (erf form) fused into the epilogue. With
+ * h = X_e @ W[e] rounded to dtype (as nt_grouped_gemm writes it), stores
+ * act = gelu(h) and act_grad = gelu'(h), both [A,N] and rounded once; h
+ * itself is not stored (the backward needs only act_grad). The reference
+ * runs grouped_gemm_kernel and then the activation
+ * (src/model/feed_fwd.py:107-112, with the configs' GELU in place of SiLU);
+ * no single reference entry point corresponds. */
+int nt_grouped_gemm_gelu(int dtype, const void* X, const int32_t* offsets, const void* W,
+                         int32_t E, int64_t A, int64_t K, int64_t N, void* act, void* act_grad,
+                         void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* dX GEMM with the GELU backward fused into the epilogue:
+ * dH = (dOut @ W[e]^T, rounded) * act_grad, rounded once, with act_grad the
+ * gelu'(h) nt_grouped_gemm_gelu stored. W [E,K,N], dOut [A,N], act_grad and
+ * dH [A,K]. Replaces bwd_grouped_gemm_dX_kernel followed by the
+ * activation's backward (reference csrc/kernels/bwd_grouped_gemm_dX.cu:46-96,
+ * then autograd). */
+int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                            const void* act_grad, int32_t E, int64_t A, int64_t K, int64_t N,
+                            void* dH, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* dW[e] = X_e^T @ dOut_e summed over the rows of expert e (zero for an empty
- * expert). X [A,K], dOut [A,N], dW [E,K,N]. Deterministic: fixed split of
- * each expert's rows, partials reduced in a fixed order.
+ * expert). X [A,K], dOut [A,N], dW [E,K,N]. Deterministic: each output tile
+ * reduces its expert's rows in a fixed order (no atomics, no split).
  * Replaces bwd_grouped_gemm_dW_kernel (reference csrc/kernels/bwd_grouped_gemm_dW.cu:43-86). */
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,

@@ -115,6 +115,23 @@ struct mfma_op<f16> {
   }
 };
 
+// Two fp32 values rounded to nearest-even and packed into 32 bits (first
+// value in the low half). bf16 uses the hardware pair conversion
+// (v_cvt_pk_bf16_f32, RNE); fp16 converts each value (v_cvt_f16_f32, RNE).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16>(float a, float b) {
+  return (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -284,7 +301,13 @@ struct GemmArgs {
   int32_t ntn;      // output tiles along the n dimension
   int32_t ntm;      // dW only: output tiles along K
   int64_t mtiles;   // m-tile slots enumerated by the grid (upper bound for fwd / dX)
+  void* out2;       // fused GELU forward: gelu'(h), same layout as out
+  const void* aux;  // fused GELU backward: gelu'(h), same layout as out
 };
+
+// Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
+// itself is not stored); backward GELU (out = C * aux, aux = gelu'(h)).
+enum GemmEpilogue { kEpiPlain = 0, kEpiGelu = 1, kEpiGeluGrad = 2 };
 
 // Logical tile -> (m-tile, n-tile): groups of kGroupM m-tiles, m fastest
 // inside a group, so neighbouring logical tiles reuse both A and B panels.
@@ -309,6 +332,8 @@ struct TileJob {
   int64_t kred;                    // reduction length
   uint16_t* po;
   int64_t ldo;
+  uint16_t* po2;          // fused GELU forward: gelu'(h) output (or null)
+  const uint16_t* paux;   // fused GELU backward: gelu'(h) input (or null)
 };
 
 // Operands and extents of logical output tile `logical` (< mtiles * ntn).
@@ -317,6 +342,8 @@ struct TileJob {
 template <int MODE, int BM, int BN>
 __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pref, int64_t mtiles,
                                           int64_t logical, TileJob& j) {
+  j.po2 = nullptr;
+  j.paux = nullptr;
   int64_t mt;
   int nt;
   tile_coords(logical, mtiles, g.ntn, mt, nt);
@@ -357,6 +384,7 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
       j.kred = g.K;
       j.po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * BN;
       j.ldo = g.N;
+      if (g.out2) j.po2 = static_cast<uint16_t*>(g.out2) + row0 * g.N + (int64_t)nt * BN;
     } else {  // kDx
       j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
       j.lda = g.N;
@@ -366,6 +394,7 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
       j.kred = g.N;
       j.po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * BN;
       j.ldo = g.K;
+      if (g.aux) j.paux = static_cast<const uint16_t*>(g.aux) + row0 * g.K + (int64_t)nt * BN;
     }
   }
 }
@@ -424,12 +453,78 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[TM][TN], const 
         const int n = n0 + jn * 32 + 8 * gq + 4 * (lane >> 5);
         if (n >= j.cols_valid) continue;
         uint2 pk;
-        pk.x = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 0]) |
-               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 1]) << 16);
-        pk.y = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 2]) |
-               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 3]) << 16);
+        pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
+        pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
         *reinterpret_cast<uint2*>(prow + n) = pk;
       }
+  }
+}
+
+// GELU, erf form, for 16-bit outputs: gelu(x) = x * Phi(x) and
+// gelu'(x) = Phi(x) + x * phi(x), with Phi the standard normal CDF,
+// Phi(x) = erfc(-x/sqrt2)/2, and phi(x) = exp(-x^2/2)/sqrt(2 pi).
+// erfc(z), z >= 0, is the Chebyshev fit of Press et al., Numerical Recipes
+// ("erfcc": t = 1/(1 + z/2), erfc(z) = t exp(-z^2 + P(t)), fractional error
+// below 1.2e-7 everywhere), evaluated with the hardware exp2 and reciprocal:
+// far below the half-ulp of bf16 / fp16 and about half the instructions of
+// the library erff. The fp32 / fp64 elementwise path uses erf / exp.
+__device__ __forceinline__ float erfc_nonneg(float z, float& ez2) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  p = fmaf(p, t, -1.26551223f);
+  ez2 = __builtin_amdgcn_exp2f(-z * z * kLog2e);           // exp(-z^2)
+  return t * ez2 * __builtin_amdgcn_exp2f(p * kLog2e);
+}
+__device__ __forceinline__ float norm_cdf(float x, float& ez2) {
+  const float c = 0.5f * erfc_nonneg(fabsf(x) * 0.70710678118654752f, ez2);
+  return x >= 0.f ? 1.0f - c : c;
+}
+// Stores 8 consecutive 16-bit outputs `v` (already rounded) at element
+// offset `o` of the tile's output rows, applying the epilogue:
+//   kEpiGelu:     out = gelu(v), out2 = gelu'(v)   (v = h, not stored)
+//   kEpiGeluGrad: out = v * aux                    (v = dA, aux = gelu'(h))
+template <typename T, int EPI>
+__device__ __forceinline__ void epilogue8(uint4 v, const TileJob& j, int64_t o) {
+  if (EPI == kEpiPlain) {
+    *reinterpret_cast<uint4*>(j.po + o) = v;
+    return;
+  }
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t r[4], r2[4];
+  if (EPI == kEpiGelu) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float x0 = elem<T>::load((uint16_t)(w[q] & 0xffffu));
+      const float x1 = elem<T>::load((uint16_t)(w[q] >> 16));
+      float e0, e1;
+      const float c0 = norm_cdf(x0, e0), c1 = norm_cdf(x1, e1);
+      r[q] = pack2<T>(x0 * c0, x1 * c1);
+      r2[q] = pack2<T>(fmaf(x0, e0 * 0.39894228040143268f, c0),
+                       fmaf(x1, e1 * 0.39894228040143268f, c1));
+    }
+    *reinterpret_cast<uint4*>(j.po + o) = make_uint4(r[0], r[1], r[2], r[3]);
+    *reinterpret_cast<uint4*>(j.po2 + o) = make_uint4(r2[0], r2[1], r2[2], r2[3]);
+  } else {
+    const uint4 gv = *reinterpret_cast<const uint4*>(j.paux + o);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float d0 = elem<T>::load((uint16_t)(w[q] & 0xffffu));
+      const float d1 = elem<T>::load((uint16_t)(w[q] >> 16));
+      const float g0 = elem<T>::load((uint16_t)(gw[q] & 0xffffu));
+      const float g1 = elem<T>::load((uint16_t)(gw[q] >> 16));
+      r[q] = pack2<T>(d0 * g0, d1 * g1);
+    }
+    *reinterpret_cast<uint4*>(j.po + o) = make_uint4(r[0], r[1], r[2], r[3]);
   }
 }
 
@@ -441,7 +536,7 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[TM][TN], const 
 // LDS operations of one wave complete in order, so no barrier is needed.
 constexpr int kEpiPitch = 136;
 constexpr int kEpiBytes = 32 * kEpiPitch;
-template <typename T, int TM, int TN>
+template <typename T, int EPI, int TM, int TN>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
                                                int m0, int n0, int lane, char* scratch) {
   static_assert(TN == 2, "64-column wave blocks");
@@ -453,10 +548,8 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
       for (int gq = 0; gq < 4; ++gq) {
         const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
         uint2 pk;
-        pk.x = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 0]) |
-               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 1]) << 16);
-        pk.y = (uint32_t)elem<T>::store(acc[i][jn][4 * gq + 2]) |
-               ((uint32_t)elem<T>::store(acc[i][jn][4 * gq + 3]) << 16);
+        pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
+        pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
         *reinterpret_cast<uint2*>(scratch + (lane & 31) * kEpiPitch + c * 2) = pk;
       }
 #pragma unroll
@@ -465,8 +558,7 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
       const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kEpiPitch + (lane & 7) * 16);
       const int m = m0 + i * 32 + rr;
       const int n = n0 + (lane & 7) * 8;
-      if (m < j.rows_valid && n < j.cols_valid)
-        *reinterpret_cast<uint4*>(j.po + (int64_t)m * j.ldo + n) = v;
+      if (m < j.rows_valid && n < j.cols_valid) epilogue8<T, EPI>(v, j, (int64_t)m * j.ldo + n);
     }
   }
 }
@@ -494,7 +586,7 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[TM][TN]) {
 // Tiles are dealt to XCDs in contiguous ranges (workgroup b runs on XCD
 // b % 8), so tiles that share operand panels share that XCD's L2; inside a
 // range, tile_coords walks groups of kGroupM m-tiles with m fastest.
-template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS>
+template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI>
 __global__ void __launch_bounds__(WGM * WGN * kWave)
 gg_mfma_kernel(GemmArgs g) {
   constexpr int NW = WGM * WGN;
@@ -615,11 +707,12 @@ gg_mfma_kernel(GemmArgs g) {
       for (int s0 = 0; s0 < NS - 1; ++s0)
         if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
     }
-    if (TN == 2) {
+    static_assert(TN == 2 || EPI == kEpiPlain, "fused epilogues use the LDS-staged store");
+    if constexpr (TN == 2) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * kEpiBytes <= kStage, "epilogue scratch fits one stage");
-      store_tile_lds<T>(acc, job, wm * WM, wn * WN, lane,
-                        smem + (NS - 1) * kStage + wave * kEpiBytes);
+      store_tile_lds<T, EPI>(acc, job, wm * WM, wn * WN, lane,
+                             smem + (NS - 1) * kStage + wave * kEpiBytes);
     } else {
       store_tile<T>(acc, job, wm * WM, wn * WN, lane);
     }
@@ -799,14 +892,14 @@ int blocks_per_cu(K kernel, int threads) {
   return n;
 }
 
-template <int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS>
+template <int MODE, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS>
 int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t tiles = plan_tiles<MODE>(g, out_cols, BM, BN);
   if (tiles == 0) return NT_OK;
   if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
   constexpr int threads = WGM * WGN * kWave;
-  auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS>;
-  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS>;
+  auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS, EPI>;
+  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS, EPI>;
   // Occupancy of this instantiation (bf16 and fp16 share resource usage).
   static const int per_cu = blocks_per_cu(kb, threads);
   // Persistent: at most one resident wave of workgroups; each walks tiles.
@@ -822,18 +915,55 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
 // Tile shape (measured on MI355X over the configs' shapes): 256x256 with 8
 // waves unless that leaves fewer than 1.5 tiles per CU, then 128x128 with 4
 // waves (two workgroups per CU).
-template <int MODE>
+template <int MODE, int EPI>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t rows = MODE == kDw ? g.K * g.E : g.A;
   const int64_t tiles256 = ceil_div(rows, 256) * ceil_div(out_cols, 256);
   if (tiles256 * 2 >= (int64_t)device_cus() * 3)
-    return launch_mfma<MODE, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
-  return launch_mfma<MODE, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
+    return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
+  return launch_mfma<MODE, EPI, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
 }
 
-template <int MODE>
+// Elementwise GELU for the generic path (fp32 / fp64, or shapes the MFMA
+// kernel does not take). Forward: io holds h on entry and gelu(h) on exit,
+// g receives gelu'(h). Backward: io holds dA on entry and dA * g on exit.
+template <typename T, bool GRAD>
+__global__ void __launch_bounds__(256) gelu_elementwise_kernel(void* io_, void* g_, int64_t n) {
+  typedef typename elem<T>::storage S;
+  typedef typename acc_type<T>::type AT;
+  S* io = static_cast<S*>(io_);
+  S* g = static_cast<S*>(g_);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (GRAD) {
+      io[i] = from_acc<T>(to_acc<T>(io[i]) * to_acc<T>(g[i]));
+    } else {
+      const AT x = to_acc<T>(io[i]);
+      const AT cdf = AT(0.5) * (AT(1) + erf(x * AT(0.70710678118654752440)));
+      const AT pdf = exp(AT(-0.5) * x * x) * AT(0.39894228040143267794);
+      g[i] = from_acc<T>(cdf + x * pdf);
+      io[i] = from_acc<T>(x * cdf);
+    }
+  }
+}
+
+template <bool GRAD>
+int launch_gelu_elementwise(int dtype, void* io, void* g, int64_t n, hipStream_t s) {
+  if (n == 0) return NT_OK;
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus() * 16));
+  switch (dtype) {
+    case NT_F32: hipLaunchKernelGGL((gelu_elementwise_kernel<float, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
+    case NT_F64: hipLaunchKernelGGL((gelu_elementwise_kernel<double, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
+    case NT_F16: hipLaunchKernelGGL((gelu_elementwise_kernel<f16, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
+    case NT_BF16: hipLaunchKernelGGL((gelu_elementwise_kernel<bf16, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
+    default: return NT_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+template <int MODE, int EPI>
 int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t s) {
-  if (mfma) return launch_mfma_auto<MODE>(dtype, g, out_cols, s);
+  if (mfma) return launch_mfma_auto<MODE, EPI>(dtype, g, out_cols, s);
   g.ntn = (int32_t)ceil_div(out_cols, kGT);
   int64_t nblocks;
   if (MODE == kDw) {
@@ -853,7 +983,13 @@ int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t 
     case NT_BF16: hipLaunchKernelGGL((gg_generic_kernel<bf16, MODE>), grid, dim3(256), 0, s, g); break;
     default: return NT_ERR_DTYPE;
   }
-  return launch_status();
+  int st = launch_status();
+  if (st != NT_OK || EPI == kEpiPlain) return st;
+  // Generic path: the GELU epilogue as a second, elementwise pass over the
+  // output rows (rows past offsets[E] hold unspecified values either way).
+  const int64_t n = g.A * out_cols;
+  if (EPI == kEpiGelu) return launch_gelu_elementwise<false>(dtype, g.out, g.out2, n, s);
+  return launch_gelu_elementwise<true>(dtype, g.out, const_cast<void*>(g.aux), n, s);
 }
 
 int check_gemm(int dtype, int32_t E, int64_t A, int64_t K, int64_t N, const void* a,
@@ -892,8 +1028,23 @@ int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void
   int st = check_gemm(dtype, E, A, K, N, X, W, offsets, out);
   if (st != NT_OK) return st;
   if (A == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0, 0};
-  return launch_mode<kFwd>(dtype, g, N, mfma_ok(dtype, K, N, X, W, out), stream);
+  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0, 0, nullptr, nullptr};
+  return launch_mode<kFwd, kEpiPlain>(dtype, g, N, mfma_ok(dtype, K, N, X, W, out), stream);
+}
+
+int nt_grouped_gemm_gelu(int dtype, const void* X, const int32_t* offsets, const void* W,
+                         int32_t E, int64_t A, int64_t K, int64_t N, void* act, void* act_grad,
+                         void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, X, W, offsets, act);
+  if (st != NT_OK) return st;
+  if (act_grad == nullptr && A > 0 && N > 0) return NT_ERR_INVALID_ARG;
+  if (A == 0 || N == 0) return NT_OK;
+  GemmArgs g{X, W, offsets, E, A, K, N, act, 0, 0, 0, act_grad, nullptr};
+  const bool mfma =
+      mfma_ok(dtype, K, N, X, W, act) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
+  return launch_mode<kFwd, kEpiGelu>(dtype, g, N, mfma, stream);
 }
 
 int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const void* dOut,
@@ -904,8 +1055,23 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
   int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
   if (st != NT_OK) return st;
   if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0};
-  return launch_mode<kDx>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr};
+  return launch_mode<kDx, kEpiPlain>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
+}
+
+int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                            const void* act_grad, int32_t E, int64_t A, int64_t K, int64_t N,
+                            void* dH, void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH);
+  if (st != NT_OK) return st;
+  if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0) return NT_OK;
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad};
+  const bool mfma =
+      mfma_ok(dtype, K, N, dOut, W, dH) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
+  return launch_mode<kDx, kEpiGeluGrad>(dtype, g, K, mfma, stream);
 }
 
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
@@ -916,8 +1082,8 @@ int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const v
   int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
   if (st != NT_OK) return st;
   if (K == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0};
-  return launch_mode<kDw>(dtype, g, N, mfma_ok(dtype, K, N, X, dOut, dW), stream);
+  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr};
+  return launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma_ok(dtype, K, N, X, dOut, dW), stream);
 }
 
 }  // extern "C"

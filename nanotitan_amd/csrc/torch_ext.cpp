@@ -284,6 +284,53 @@ Tensor bwd_grouped_gemm_dX_kernel(Tensor W, Tensor offsets, Tensor dOut) {
   return dX;
 }
 
+// grouped_gemm_gelu(X, expert_offset, W_up) -> (gelu(h), gelu'(h)), both
+// [A, N], h = X @ W_up per expert: the up-projection with the activation
+// fused into its epilogue.
+std::tuple<Tensor, Tensor> grouped_gemm_gelu(Tensor X, Tensor offsets, Tensor W) {
+  check_gemm_inputs(X, offsets, W);
+  TORCH_CHECK(X.dim() == 2 && W.dim() == 3 && W.size(1) == X.size(1),
+              "expected X [A,K] and weights [E,K,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = X.size(0), K = X.size(1), N = W.size(2);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor act = at::empty({A, N}, X.options());
+  Tensor act_grad = at::empty({A, N}, X.options());
+  const int dt = dtype_code(X);
+  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_gelu(dt, X.data_ptr(), offsets.data_ptr<int32_t>(), W.data_ptr(), E,
+                                    A, K, N, act.data_ptr(), act_grad.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), stream_of(X)),
+               "grouped_gemm_gelu");
+  return {act, act_grad};
+}
+
+// bwd_grouped_gemm_dX_gelu(W_down, expert_offset, dOut, act_grad) -> dH [A, K]:
+// (dOut @ W^T) * gelu'(h) in one kernel.
+Tensor bwd_grouped_gemm_dX_gelu(Tensor W, Tensor offsets, Tensor dOut, Tensor act_grad) {
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(W.dim() == 3 && dOut.dim() == 2 && dOut.size(1) == W.size(2),
+              "expected W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  TORCH_CHECK(act_grad.is_contiguous() && act_grad.dim() == 2 &&
+                  act_grad.size(0) == dOut.size(0) && act_grad.size(1) == W.size(1) &&
+                  act_grad.scalar_type() == W.scalar_type(),
+              "expected act_grad [A,K] contiguous, in the weights' dtype");
+  check_device(act_grad, "act_grad");
+  const int64_t A = dOut.size(0), K = W.size(1), N = W.size(2);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(W.get_device());
+  Tensor dH = at::empty({A, K}, W.options());
+  const int dt = dtype_code(W);
+  Tensor ws = workspace(W, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dx_gelu(dt, W.data_ptr(), offsets.data_ptr<int32_t>(),
+                                       dOut.data_ptr(), act_grad.data_ptr(), E, A, K, N,
+                                       dH.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(W)),
+               "bwd_grouped_gemm_dX_gelu");
+  return dH;
+}
+
 // ------------------------------------------------------- layer extensions
 
 // Fused router gate: (gates [T,k] f32, topk [T,k] i32).
@@ -440,6 +487,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Expert-grouped GEMM weight gradient");
   m.def("bwd_grouped_gemm_dX_kernel", &bwd_grouped_gemm_dX_kernel,
         "Expert-grouped GEMM input gradient");
+  m.def("grouped_gemm_gelu", &grouped_gemm_gelu,
+        "Up-projection grouped GEMM with fused GELU -> (gelu(h), gelu'(h))");
+  m.def("bwd_grouped_gemm_dX_gelu", &bwd_grouped_gemm_dX_gelu,
+        "dX grouped GEMM with fused GELU backward -> (dOut @ W^T) * act_grad");
   m.def("dispatch_tokens", &dispatch_tokens,
         "Fused count + offsets + pack -> (counts, offsets, packed_X, token_id, expert, packed_w, inv)");
   m.def("pack_tokens_inv", &pack_tokens_inv, "pack_tokens_kernel that also returns the inverse map");

@@ -11,7 +11,7 @@
 * ``ExpertFFN(cfg, spec)`` — SwiGLU experts with ``[E,d,f]`` / ``[E,f,d]``
   weights (src/model/feed_fwd.py:39-122), three grouped GEMMs.
 * ``GeluExpertFFN(cfg, spec)`` — the 2-GEMM up -> GELU -> down FFN the
-  benchmark configs specify.
+  benchmark configs specify, with the activation fused into the GEMMs.
 * ``MoE(cfg, spec)`` — router + experts + backend (src/model/feed_fwd.py:128-152).
 * ``route(logits, top_k)`` — fp32 softmax, top-k with ties to the lower
   expert id, renormalised gates, int32 ids.
@@ -27,7 +27,13 @@ import torch
 import torch.nn as nn
 from torch.profiler import record_function
 
-from nanotitan_amd.moe_ops import combine_inv_fn, dispatch_fn, grouped_gemm_fn, route_fn
+from nanotitan_amd.moe_ops import (
+    combine_inv_fn,
+    dispatch_fn,
+    grouped_gelu_ffn_fn,
+    grouped_gemm_fn,
+    route_fn,
+)
 
 HIP_BACKENDS = ("hip", "cuda")  # "cuda" is accepted so reference configs select this path
 
@@ -125,8 +131,7 @@ class GeluExpertFFN(nn.Module):
         self.W_down = nn.Parameter(torch.randn(E, f, d).mul_(std).to(cfg.dtype))
 
     def forward(self, packed_X, expert_offset):
-        h = torch.nn.functional.gelu(grouped_gemm_fn(packed_X, self.W_up, expert_offset))
-        return grouped_gemm_fn(h, self.W_down, expert_offset)
+        return grouped_gelu_ffn_fn(packed_X, self.W_up, self.W_down, expert_offset)
 
 
 def moe_forward_from_logits(x_flat, logits, experts, num_experts, top_k):

@@ -132,6 +132,48 @@ class GroupedGEMM_FN(torch.autograd.Function):
         return dX, None, dW
 
 
+class GroupedGeluFFN_FN(torch.autograd.Function):
+    """Expert FFN up -> GELU (erf) -> down on the grouped GEMM, activation fused.
+
+    Forward: (a, g) = grouped_gemm_gelu(X, W_up) — a = gelu(h) and
+    g = gelu'(h) for h = X W_up, from one kernel — then y = a W_down.
+    Backward: dH = (dy W_down^T) * g from one kernel, then the three
+    remaining grouped GEMMs. The values of grouped_gemm_fn +
+    torch.nn.functional.gelu + grouped_gemm_fn (the reference's ExpertFFN
+    dataflow, src/model/feed_fwd.py:102-112, with the configs' GELU), except
+    that gelu'(h) is rounded to the activation dtype before the multiply;
+    backward returns (dX, None, dW_up, dW_down).
+    """
+
+    @staticmethod
+    def forward(ctx, X, expert_offset, W_up, W_down):
+        ext = get_hip_extension()
+        a, g = ext.grouped_gemm_gelu(X, expert_offset, W_up)
+        y = ext.grouped_gemm_kernel(a, expert_offset, W_down)
+        ctx.save_for_backward(X, expert_offset, W_up, W_down, a, g)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        ext = get_hip_extension()
+        X, expert_offset, W_up, W_down, a, g = ctx.saved_tensors
+        dy = dy.contiguous()
+        dX = dW_up = dW_down = None
+        if ctx.needs_input_grad[3]:
+            dW_down = ext.bwd_grouped_gemm_dW_kernel(a, expert_offset, dy)
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[2]:
+            dH = ext.bwd_grouped_gemm_dX_gelu(W_down, expert_offset, dy, g)
+            if ctx.needs_input_grad[0]:
+                dX = ext.bwd_grouped_gemm_dX_kernel(W_up, expert_offset, dH)
+            if ctx.needs_input_grad[2]:
+                dW_up = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dH)
+        return dX, None, dW_up, dW_down
+
+
+def grouped_gelu_ffn_fn(X, W_up, W_down, expert_offset):
+    return GroupedGeluFFN_FN.apply(X, expert_offset, W_up, W_down)
+
+
 # --------------------------------------------------------------- layer ops
 
 
