@@ -312,11 +312,15 @@ def main():
     prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
     if prof.exists():
         fams_t = json.loads(prof.read_text()).get("families", {})
-        gemm_t = [fams_t[f] for f in ("gemm_fwd", "gemm_dx", "gemm_dw") if f in fams_t]
-        if gemm_t:
-            roofline["traffic"] = round(sum(t["bytes"] for t in gemm_t) / len(gemm_t))
+        # GEMM launches of one step: up (fused GELU), down, down dX (fused
+        # GELU backward), up dX, and two dW; traffic per launch averaged over them.
+        per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_dx_gelu": 1, "gemm_dx": 1,
+                    "gemm_dw": 2}
+        if all(f in fams_t for f in per_step):
+            n = sum(per_step.values())
+            roofline["traffic"] = round(sum(fams_t[f]["bytes"] * c for f, c in per_step.items()) / n)
             roofline["traffic_algorithmic"] = round(
-                sum(t["algorithmic_bytes"] for t in gemm_t) / len(gemm_t))
+                sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
             roofline["traffic_source"] = f"profiles/{prof.name}"
     kernels = {}
     for fam, r in fams.items():

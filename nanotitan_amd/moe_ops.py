@@ -193,12 +193,16 @@ class DispatchFN(torch.autograd.Function):
         )
         ctx.save_for_backward(inv)
         ctx.mark_non_differentiable(counts, offsets, token_id, inv)
+        # No zero-filled grads for the integer outputs (or an unused packed_w).
+        ctx.set_materialize_grads(False)
         return packed_X, packed_w, counts, offsets, token_id, inv
 
     @staticmethod
     def backward(ctx, packed_X_grad, packed_w_grad, *_):
         ext = get_hip_extension()
         (inv,) = ctx.saved_tensors
+        if packed_X_grad is None:
+            raise RuntimeError("dispatch_fn backward needs a gradient for packed_X")
         if packed_w_grad is None:
             packed_w_grad = torch.zeros(inv.numel(), dtype=torch.float32, device=inv.device)
         X_grad, w_grad = ext.pack_backward_inv(
@@ -246,6 +250,7 @@ class RouteFN(torch.autograd.Function):
         ctx.save_for_backward(gates, topk)
         ctx.num_experts = logits.shape[1]
         ctx.mark_non_differentiable(topk)
+        ctx.set_materialize_grads(False)  # no zero-filled grad for the int32 ids
         return gates, topk
 
     @staticmethod
