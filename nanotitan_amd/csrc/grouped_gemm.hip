@@ -65,6 +65,48 @@ __device__ void build_m_prefix(const int32_t* __restrict__ offsets, int E, int64
   __syncthreads();
 }
 
+// dW reduction chunks. Expert e's rows are cut into nch(e) = max(1,
+// ceil(M_e / R)) chunks of R rows (an empty expert keeps one empty chunk, so
+// its dW is still written, as zeros). s_pref[e] = chunks of experts < e;
+// s_split[e] = chunks of experts < e that have at least two (those write
+// fp32 partials, one slab per chunk, and a reduce pass sums them in chunk
+// order). R = 0 means one chunk per expert. Ends with a workgroup barrier.
+__device__ __forceinline__ int dw_chunks(int64_t rows, int32_t R) {
+  if (R <= 0) return 1;
+  const int n = (int)ceil_div(rows, R);
+  return n < 1 ? 1 : n;
+}
+__device__ void build_chunk_prefix(const int32_t* __restrict__ offsets, int E, int64_t A,
+                                   int32_t R, int32_t* s_pref, int32_t* s_split) {
+  if (threadIdx.x < kWave) {
+    const int lane = lane_id();
+    int carry = 0, carry_s = 0;
+    for (int s = 0; s < E; s += kWave) {
+      const int e = s + lane;
+      int v = 0, vs = 0;
+      if (e < E) {
+        int64_t a, b;
+        expert_rows(offsets, e, A, a, b);
+        v = dw_chunks(b - a, R);
+        vs = v >= 2 ? v : 0;
+      }
+      const int incl = wave_incl_scan(v);
+      const int incl_s = wave_incl_scan(vs);
+      if (e < E) {
+        s_pref[e + 1] = carry + incl;
+        s_split[e + 1] = carry_s + incl_s;
+      }
+      carry += __shfl(incl, kWave - 1, kWave);
+      carry_s += __shfl(incl_s, kWave - 1, kWave);
+    }
+    if (lane == 0) {
+      s_pref[0] = 0;
+      s_split[0] = 0;
+    }
+  }
+  __syncthreads();
+}
+
 // Expert owning m-tile `mt_global` (expert-major order) and the tile's row
 // range; false when mt_global is past the last tile.
 __device__ bool find_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A,
@@ -303,6 +345,8 @@ struct GemmArgs {
   int64_t mtiles;   // m-tile slots enumerated by the grid (upper bound for fwd / dX)
   void* out2;       // fused GELU forward: gelu'(h), same layout as out
   const void* aux;  // fused GELU backward: gelu'(h), same layout as out
+  int32_t chunk;    // dW: rows per reduction chunk (0: one chunk per expert)
+  float* partial;   // dW: fp32 partial slabs [split chunks][K][N] when chunk > 0
 };
 
 // Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
@@ -334,6 +378,7 @@ struct TileJob {
   int64_t ldo;
   uint16_t* po2;          // fused GELU forward: gelu'(h) output (or null)
   const uint16_t* paux;   // fused GELU backward: gelu'(h) input (or null)
+  float* pf;              // dW of a split expert: fp32 partial slab origin (or null)
 };
 
 // Operands and extents of logical output tile `logical` (< mtiles * ntn).
@@ -344,27 +389,40 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
                                           int64_t logical, TileJob& j) {
   j.po2 = nullptr;
   j.paux = nullptr;
+  j.pf = nullptr;
   int64_t mt;
   int nt;
   tile_coords(logical, mtiles, g.ntn, mt, nt);
   if (MODE == kDw) {
-    const int e = (int)(mt / g.ntm);
+    // m-tile = (reduction chunk, K tile); s_pref / s_split: build_chunk_prefix.
+    const int32_t* s_split = s_pref + (NT_MAX_EXPERTS + 1);
+    const int64_t cg = mt / g.ntm;
     const int mtl = (int)(mt % g.ntm);
-    int64_t r0, r1;
-    expert_rows(g.offsets, e, g.A, r0, r1);
+    int e;
+    int64_t r0, r1, c;
+    find_m_tile(g.offsets, g.E, g.A, s_pref, cg, e, r0, r1, c);
     // Uniform across the workgroup (read from HBM / LDS): keep them scalar.
+    e = __builtin_amdgcn_readfirstlane(e);
     r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
     r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
-    j.kred = r1 - r0;
-    j.pa = static_cast<const uint16_t*>(g.a) + r0 * g.K + (int64_t)mtl * BM;
+    c = (int64_t)__builtin_amdgcn_readfirstlane((int)c);
+    const int nch = s_pref[e + 1] - s_pref[e];
+    int64_t c0 = r0, c1 = r1;
+    if (g.chunk > 0) {
+      c0 = r0 + c * g.chunk;
+      c1 = c0 + g.chunk < r1 ? c0 + g.chunk : r1;
+    }
+    j.kred = c1 - c0;
+    j.pa = static_cast<const uint16_t*>(g.a) + c0 * g.K + (int64_t)mtl * BM;
     j.lda = g.K;
-    j.pb = static_cast<const uint16_t*>(g.b) + r0 * g.N + (int64_t)nt * BN;
+    j.pb = static_cast<const uint16_t*>(g.b) + c0 * g.N + (int64_t)nt * BN;
     j.ldb = g.N;
     j.rows_valid = g.K - (int64_t)mtl * BM;
     j.cols_valid = g.N - (int64_t)nt * BN;
-    j.po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + (int64_t)mtl * BM * g.N +
-           (int64_t)nt * BN;
+    const int64_t tile_off = (int64_t)mtl * BM * g.N + (int64_t)nt * BN;
+    j.po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + tile_off;
     j.ldo = g.N;
+    if (nch >= 2) j.pf = g.partial + (int64_t)(s_split[e] + c) * g.K * g.N + tile_off;
   } else {
     int e;
     int64_t r0, r1, mtl;
@@ -528,38 +586,79 @@ __device__ __forceinline__ void epilogue8(uint4 v, const TileJob& j, int64_t o) 
   }
 }
 
-// Epilogue through LDS for 64-column wave blocks: each 32-row sub-tile is
-// rounded (RNE), written to this wave's LDS scratch (32 rows, 136-byte
-// pitch: the 8-byte writes of 32 rows fall on distinct banks), and read back
-// 16 bytes per lane so that every store instruction writes 8 whole
-// 128-byte row segments. `scratch` is 32 * 136 bytes private to the wave;
-// LDS operations of one wave complete in order, so no barrier is needed.
-constexpr int kEpiPitch = 136;
-constexpr int kEpiBytes = 32 * kEpiPitch;
-template <typename T, int EPI, int TM, int TN>
+// Epilogue through LDS for 64- or 128-column wave blocks (TN = 2 or 4):
+// each 32-row sub-tile is rounded (RNE), written to this wave's LDS scratch
+// (pitch 32*TN*2 + 8 bytes: the 8-byte writes of 32 rows fall on distinct
+// banks), and read back 16 bytes per lane so that every store instruction
+// writes whole 128- or 256-byte row segments. `scratch` is
+// epi_bytes<TN, ROWS>() bytes private to the wave; LDS operations of one
+// wave complete in order, so no barrier is needed. With ROWS = 16 the
+// sub-tile goes through in two halves (lanes 0-15 and 32-47 hold rows 0-15,
+// the others rows 16-31), halving the scratch.
+template <int TN>
+constexpr int epi_pitch() { return 64 * TN + 8; }
+template <int TN, int ROWS>
+constexpr int epi_bytes() { return ROWS * epi_pitch<TN>(); }
+template <typename T, int EPI, int ROWS, int TM, int TN>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
                                                int m0, int n0, int lane, char* scratch) {
-  static_assert(TN == 2, "64-column wave blocks");
+  static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
+  static_assert(ROWS == 32 || ROWS == 16, "32 or 16 scratch rows");
+  constexpr int kPitch = epi_pitch<TN>();
+  constexpr int kPasses = 32 / ROWS;
+  constexpr int kLanesPerRow = TN * 4;       // 16-byte chunks per row
+  constexpr int kRowsPerRead = 64 / kLanesPerRow;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int r = lane & 31;
+      const bool mine = kPasses == 1 || (r / ROWS) == ps;
+      if (mine) {
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
+            uint2 pk;
+            pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
+            pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
+            *reinterpret_cast<uint2*>(scratch + (r % ROWS) * kPitch + c * 2) = pk;
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < ROWS / kRowsPerRead; ++q) {
+        const int rr = q * kRowsPerRead + lane / kLanesPerRow;
+        const int ch = lane % kLanesPerRow;
+        const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kPitch + ch * 16);
+        const int m = m0 + i * 32 + ps * ROWS + rr;
+        const int n = n0 + ch * 8;
+        if (m < j.rows_valid && n < j.cols_valid) epilogue8<T, EPI>(v, j, (int64_t)m * j.ldo + n);
+      }
+    }
+  }
+}
+
+// fp32 partial of a split dW tile: each lane stores its 4 consecutive
+// columns of a row as one 16-byte write; the reduce pass rounds later.
+template <int TM, int TN>
+__device__ __forceinline__ void store_partial(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+                                              int m0, int n0, int lane) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + i * 32 + (lane & 31);
+    if (m >= j.rows_valid) continue;
+    float* prow = j.pf + (int64_t)m * j.ldo;
 #pragma unroll
     for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
-        uint2 pk;
-        pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
-        pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
-        *reinterpret_cast<uint2*>(scratch + (lane & 31) * kEpiPitch + c * 2) = pk;
+        const int n = n0 + jn * 32 + 8 * gq + 4 * (lane >> 5);
+        if (n >= j.cols_valid) continue;
+        *reinterpret_cast<float4*>(prow + n) =
+            make_float4(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1], acc[i][jn][4 * gq + 2],
+                        acc[i][jn][4 * gq + 3]);
       }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int rr = q * 8 + (lane >> 3);
-      const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kEpiPitch + (lane & 7) * 16);
-      const int m = m0 + i * 32 + rr;
-      const int n = n0 + (lane & 7) * 8;
-      if (m < j.rows_valid && n < j.cols_valid) epilogue8<T, EPI>(v, j, (int64_t)m * j.ldo + n);
-    }
   }
 }
 
@@ -600,12 +699,16 @@ gg_mfma_kernel(GemmArgs g) {
   constexpr int kStage = Loader::TA::kBytes + Loader::TB::kBytes;
   constexpr int kLoadsPerStage = Loader::TA::kPer + Loader::TB::kPer;  // per wave
   __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
-  __shared__ int32_t s_pref[NT_MAX_EXPERTS + 1];
+  // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
+  __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
 
-  int64_t mtiles = g.mtiles;
+  int64_t mtiles;
   if (MODE != kDw) {
     build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
     mtiles = s_pref[g.E];
+  } else {
+    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, s_pref, s_pref + (NT_MAX_EXPERTS + 1));
+    mtiles = (int64_t)s_pref[g.E] * g.ntm;
   }
   const int64_t total = mtiles * g.ntn;
   constexpr int kXcd = 8;
@@ -707,12 +810,16 @@ gg_mfma_kernel(GemmArgs g) {
       for (int s0 = 0; s0 < NS - 1; ++s0)
         if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
     }
-    static_assert(TN == 2 || EPI == kEpiPlain, "fused epilogues use the LDS-staged store");
-    if constexpr (TN == 2) {
+    static_assert(TN == 2 || TN == 4 || EPI == kEpiPlain,
+                  "fused epilogues use the LDS-staged store");
+    if (MODE == kDw && job.pf != nullptr) {
+      store_partial(acc, job, wm * WM, wn * WN, lane);
+    } else if constexpr (TN == 2 || TN == 4) {
       // The ring's last slot is idle until the next tile's first iteration.
-      static_assert(NW * kEpiBytes <= kStage, "epilogue scratch fits one stage");
-      store_tile_lds<T, EPI>(acc, job, wm * WM, wn * WN, lane,
-                             smem + (NS - 1) * kStage + wave * kEpiBytes);
+      constexpr int kRows = NW * epi_bytes<TN, 32>() <= kStage ? 32 : 16;
+      static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
+      store_tile_lds<T, EPI, kRows>(acc, job, wm * WM, wn * WN, lane,
+                                    smem + (NS - 1) * kStage + wave * epi_bytes<TN, kRows>());
     } else {
       store_tile<T>(acc, job, wm * WM, wn * WN, lane);
     }
@@ -875,7 +982,9 @@ int64_t plan_tiles(GemmArgs& g, int64_t out_cols, int BM, int BN) {
   g.ntn = (int32_t)ceil_div(out_cols, BN);
   if (MODE == kDw) {
     g.ntm = (int32_t)ceil_div(g.K, BM);
-    g.mtiles = (int64_t)g.E * g.ntm;
+    // Chunks: at most one per expert plus A / chunk (upper bound).
+    const int64_t chunks = g.chunk > 0 ? g.E + g.A / g.chunk : g.E;
+    g.mtiles = chunks * g.ntm;
   } else {
     g.ntm = 0;
     g.mtiles = ceil_div(g.A, BM) + g.E;  // upper bound: each expert's last tile may be partial
@@ -917,8 +1026,10 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
 // waves (two workgroups per CU).
 template <int MODE, int EPI>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
-  const int64_t rows = MODE == kDw ? g.K * g.E : g.A;
-  const int64_t tiles256 = ceil_div(rows, 256) * ceil_div(out_cols, 256);
+  const int64_t chunks = g.chunk > 0 ? g.E + g.A / g.chunk : g.E;
+  const int64_t tiles256 = MODE == kDw
+                               ? chunks * ceil_div(g.K, 256) * ceil_div(out_cols, 256)
+                               : ceil_div(g.A, 256) * ceil_div(out_cols, 256);
   if (tiles256 * 2 >= (int64_t)device_cus() * 3)
     return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
   return launch_mfma<MODE, EPI, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
@@ -959,6 +1070,80 @@ int launch_gelu_elementwise(int dtype, void* io, void* g, int64_t n, hipStream_t
     default: return NT_ERR_DTYPE;
   }
   return launch_status();
+}
+
+// Split dW: dW[e] = sum over its chunks, in chunk order, of the fp32
+// partial slabs, rounded once. Only experts with two or more chunks; the
+// others were written by the GEMM. Grid: (element blocks, E).
+template <typename T>
+__global__ void __launch_bounds__(256)
+dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int32_t R,
+                 const float* __restrict__ partial, int64_t KN,
+                 typename elem<T>::storage* __restrict__ dW) {
+  __shared__ int32_t s_info[2];
+  const int e = blockIdx.y;
+  if (threadIdx.x < kWave) {
+    const int lane = lane_id();
+    int before = 0;
+    for (int s0 = 0; s0 < e; s0 += kWave) {
+      const int ee = s0 + lane;
+      int v = 0;
+      if (ee < e) {
+        int64_t a, b;
+        expert_rows(offsets, ee, A, a, b);
+        v = dw_chunks(b - a, R);
+        v = v >= 2 ? v : 0;
+      }
+      before += wave_sum_int(v);
+    }
+    if (lane == 0) {
+      int64_t a, b;
+      expert_rows(offsets, e, A, a, b);
+      s_info[0] = before;
+      s_info[1] = dw_chunks(b - a, R);
+    }
+  }
+  __syncthreads();
+  const int nch = s_info[1];
+  if (nch < 2) return;
+  const float* base = partial + (int64_t)s_info[0] * KN;
+  typename elem<T>::storage* out = dW + (int64_t)e * KN;
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < KN;
+       i += (int64_t)gridDim.x * blockDim.x * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nch; ++c) {
+      const float4 u = *reinterpret_cast<const float4*>(base + (int64_t)c * KN + i);
+      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)c * KN + i + 4);
+      acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
+      acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
+    }
+    uint4 r;
+    r.x = (uint32_t)elem<T>::store(acc[0]) | ((uint32_t)elem<T>::store(acc[1]) << 16);
+    r.y = (uint32_t)elem<T>::store(acc[2]) | ((uint32_t)elem<T>::store(acc[3]) << 16);
+    r.z = (uint32_t)elem<T>::store(acc[4]) | ((uint32_t)elem<T>::store(acc[5]) << 16);
+    r.w = (uint32_t)elem<T>::store(acc[6]) | ((uint32_t)elem<T>::store(acc[7]) << 16);
+    *reinterpret_cast<uint4*>(out + i) = r;
+  }
+}
+
+// Rows per dW reduction chunk: at least twice the mean expert size and
+// 1024, and large enough that the fp32 partial slabs of the split experts
+// (fewer than 2A/R of them) fit kDwBudget bytes. 0: no expert can split.
+constexpr int64_t kDwBudget = int64_t(64) << 20;
+int32_t dw_chunk_rows(int64_t A, int64_t K, int64_t N, int32_t E) {
+  const int64_t slab = K * N * 4;
+  if (A <= 0 || slab <= 0 || E <= 0) return 0;
+  if (slab >= kDwBudget) return 0;  // R would exceed 2A: no expert can split
+  int64_t R = ceil_div(2 * A * slab, kDwBudget);
+  R = std::max<int64_t>(R, 2 * ceil_div(A, E));
+  R = round_up(std::max<int64_t>(R, 1024), 64);
+  if (R >= A) return 0;
+  return (int32_t)R;
+}
+size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
+  const int32_t R = dw_chunk_rows(A, K, N, E);
+  if (R == 0) return 0;
+  return (size_t)ceil_div(2 * A, R) * (size_t)(K * N * 4);
 }
 
 template <int MODE, int EPI>
@@ -1012,12 +1197,9 @@ using namespace nt;
 extern "C" {
 
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N) {
-  (void)dtype;
-  (void)E;
-  (void)A;
-  (void)K;
-  (void)N;
-  return 0;
+  if (dtype != NT_BF16 && dtype != NT_F16) return 0;
+  if (E < 1 || A < 0 || K < 0 || N < 0) return 0;
+  return dw_ws_bytes(A, K, N, E);
 }
 
 int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void* W, int32_t E,
@@ -1028,7 +1210,7 @@ int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void
   int st = check_gemm(dtype, E, A, K, N, X, W, offsets, out);
   if (st != NT_OK) return st;
   if (A == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0, 0, nullptr, nullptr};
+  GemmArgs g{X, W, offsets, E, A, K, N, out, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   return launch_mode<kFwd, kEpiPlain>(dtype, g, N, mfma_ok(dtype, K, N, X, W, out), stream);
 }
 
@@ -1041,7 +1223,7 @@ int nt_grouped_gemm_gelu(int dtype, const void* X, const int32_t* offsets, const
   if (st != NT_OK) return st;
   if (act_grad == nullptr && A > 0 && N > 0) return NT_ERR_INVALID_ARG;
   if (A == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, W, offsets, E, A, K, N, act, 0, 0, 0, act_grad, nullptr};
+  GemmArgs g{X, W, offsets, E, A, K, N, act, 0, 0, 0, act_grad, nullptr, 0, nullptr};
   const bool mfma =
       mfma_ok(dtype, K, N, X, W, act) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
   return launch_mode<kFwd, kEpiGelu>(dtype, g, N, mfma, stream);
@@ -1055,7 +1237,7 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
   int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
   if (st != NT_OK) return st;
   if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr};
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   return launch_mode<kDx, kEpiPlain>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
 }
 
@@ -1068,7 +1250,7 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
   if (st != NT_OK) return st;
   if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
   if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad};
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad, 0, nullptr};
   const bool mfma =
       mfma_ok(dtype, K, N, dOut, W, dH) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
   return launch_mode<kDx, kEpiGeluGrad>(dtype, g, K, mfma, stream);
@@ -1077,13 +1259,31 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
-  (void)ws;
-  (void)ws_bytes;
   int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
   if (st != NT_OK) return st;
   if (K == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr};
-  return launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma_ok(dtype, K, N, X, dOut, dW), stream);
+  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
+  const bool mfma = mfma_ok(dtype, K, N, X, dOut, dW);
+  // Split long reductions (skewed experts) when the caller's workspace holds
+  // the partial slabs; without it every expert is one chunk.
+  const int32_t R = mfma ? dw_chunk_rows(A, K, N, E) : 0;
+  const bool split = R > 0 && ws != nullptr && ws_bytes >= dw_ws_bytes(A, K, N, E) &&
+                     reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+  if (split) {
+    g.chunk = R;
+    g.partial = static_cast<float*>(ws);
+  }
+  st = launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma, stream);
+  if (st != NT_OK || !split) return st;
+  const int64_t KN = K * N;
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(KN, 256 * 8), 64), (unsigned)E);
+  if (dtype == NT_BF16)
+    hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, R,
+                       static_cast<const float*>(ws), KN, static_cast<uint16_t*>(dW));
+  else
+    hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, R,
+                       static_cast<const float*>(ws), KN, static_cast<uint16_t*>(dW));
+  return launch_status();
 }
 
 }  // extern "C"

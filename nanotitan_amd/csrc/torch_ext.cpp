@@ -238,9 +238,9 @@ Tensor grouped_gemm_kernel(Tensor X, Tensor offsets, Tensor W) {
   c10::hip::HIPGuard guard(X.get_device());
   Tensor out = at::empty({A, N}, X.options());
   const int dt = dtype_code(X);
-  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  // The forward and dX GEMMs need no workspace (only the dW split does).
   check_status(nt_grouped_gemm(dt, X.data_ptr(), offsets.data_ptr<int32_t>(), W.data_ptr(), E, A,
-                               K, N, out.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(X)),
+                               K, N, out.data_ptr(), nullptr, 0, stream_of(X)),
                "grouped_gemm_kernel");
   return out;
 }
@@ -276,10 +276,8 @@ Tensor bwd_grouped_gemm_dX_kernel(Tensor W, Tensor offsets, Tensor dOut) {
   c10::hip::HIPGuard guard(W.get_device());
   Tensor dX = at::empty({A, K}, W.options());
   const int dt = dtype_code(W);
-  Tensor ws = workspace(W, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
   check_status(nt_grouped_gemm_dx(dt, W.data_ptr(), offsets.data_ptr<int32_t>(), dOut.data_ptr(),
-                                  E, A, K, N, dX.data_ptr(), ws.data_ptr(), ws.numel(),
-                                  stream_of(W)),
+                                  E, A, K, N, dX.data_ptr(), nullptr, 0, stream_of(W)),
                "bwd_grouped_gemm_dX_kernel");
   return dX;
 }
@@ -298,10 +296,9 @@ std::tuple<Tensor, Tensor> grouped_gemm_gelu(Tensor X, Tensor offsets, Tensor W)
   Tensor act = at::empty({A, N}, X.options());
   Tensor act_grad = at::empty({A, N}, X.options());
   const int dt = dtype_code(X);
-  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
   check_status(nt_grouped_gemm_gelu(dt, X.data_ptr(), offsets.data_ptr<int32_t>(), W.data_ptr(), E,
-                                    A, K, N, act.data_ptr(), act_grad.data_ptr(), ws.data_ptr(),
-                                    ws.numel(), stream_of(X)),
+                                    A, K, N, act.data_ptr(), act_grad.data_ptr(), nullptr, 0,
+                                    stream_of(X)),
                "grouped_gemm_gelu");
   return {act, act_grad};
 }
@@ -323,10 +320,9 @@ Tensor bwd_grouped_gemm_dX_gelu(Tensor W, Tensor offsets, Tensor dOut, Tensor ac
   c10::hip::HIPGuard guard(W.get_device());
   Tensor dH = at::empty({A, K}, W.options());
   const int dt = dtype_code(W);
-  Tensor ws = workspace(W, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
   check_status(nt_grouped_gemm_dx_gelu(dt, W.data_ptr(), offsets.data_ptr<int32_t>(),
                                        dOut.data_ptr(), act_grad.data_ptr(), E, A, K, N,
-                                       dH.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(W)),
+                                       dH.data_ptr(), nullptr, 0, stream_of(W)),
                "bwd_grouped_gemm_dX_gelu");
   return dH;
 }

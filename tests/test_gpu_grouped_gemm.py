@@ -139,3 +139,41 @@ def test_gemm_is_deterministic(ext):
     a = ext.bwd_grouped_gemm_dW_kernel(X, offsets, G)
     b = ext.bwd_grouped_gemm_dW_kernel(X, offsets, G)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("counts", [[30000, 7, 0, 4000, 3000, 993, 0, 2000],
+                                    [0, 0, 45000, 0, 5000]])
+def test_dw_split_reduction_for_skewed_experts(ext, dtype, counts):
+    """A head expert far above the mean is reduced in chunks (fp32 partials in
+    the workspace, summed in chunk order by a second kernel); every expert,
+    split or not, empty or not, matches the oracle, and the result is
+    bit-identical run to run and equal to the unsplit C-ABI result within
+    one summation-order rounding."""
+    from nanotitan_amd import capi
+
+    g = torch.Generator().manual_seed(21)
+    A, K, N = sum(counts), 64, 128
+    X = torch.randn(A, K, generator=g).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    offsets = torch.zeros(len(counts) + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    E = len(counts)
+    lib = capi.load()
+    code = capi.NT_BF16 if dtype == torch.bfloat16 else capi.NT_F16
+    assert lib.nt_grouped_gemm_workspace_bytes(code, E, A, K, N) > 0  # splitting is possible
+    Xg, Gg, og = X.cuda(), G.cuda(), offsets.cuda()
+    a = ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg)
+    b = ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg)
+    # Same GEMM without a workspace: every expert in one chunk.
+    c = torch.empty_like(a)
+    st = lib.nt_grouped_gemm_dw(code, Xg.data_ptr(), og.data_ptr(), Gg.data_ptr(), E, A, K, N,
+                                c.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert st == 0
+    assert torch.equal(a, b)
+    check(a, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(counts) ** 0.5)
+    check(c, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(counts) ** 0.5)
+    for e, n in enumerate(counts):
+        if n == 0:
+            assert not a[e].any()
