@@ -69,13 +69,16 @@ def _hipcc() -> str:
 def build_library(verbose: bool = False) -> Path:
     """Compile every .hip source for gfx950 and link libnanotitan_moe.so."""
     BUILD_DIR.mkdir(exist_ok=True)
+    # Generated sources (lookup tables) go to the build folder.
+    _run([sys.executable, str(CSRC / "gen_gelu_table.py"), str(BUILD_DIR / "gelu_table_bf16.inc")],
+         verbose)
     hipcc = _hipcc()
     objs = []
     cmds = []
     for src in HIP_SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{BUILD_DIR}", "-c", str(CSRC / src), "-o", str(obj)])
     with ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB.with_suffix(".so.tmp")

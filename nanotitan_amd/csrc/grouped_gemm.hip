@@ -20,10 +20,14 @@
 // LDS-tiled FMA kernel with the same scheduler.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace nt {
 namespace {
+
+#include "gelu_table_bf16.inc"
 
 enum GemmMode { kFwd = 0, kDx = 1, kDw = 2 };
 
@@ -221,12 +225,32 @@ __device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t voff, uint3
       : "memory", "m0");
 }
 
-// Wait until at most N of this wave's vector-memory loads are in flight
-// (they retire in issue order, so the older ones are complete).
+// Wait until at most N of this wave's vector-memory operations are in
+// flight. The counter retires loads and stores in issue order, so every
+// older operation is complete.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Buffer descriptor for the epilogue's stores to one output tile. Lanes
+// outside the tile store at offset kOob, which the range check drops, so
+// every wave issues the same number of store instructions per tile (the
+// next tile's first wait counts them).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32))
+                      << 32);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0, 0x7ffffff0,
+                                           (int)kBufConfig);
+}
+
+__device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t d = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(d, r, (int)off, 0, 0);
 }
 
 // One operand tile in LDS, ROWS (m or n) x BK (reduction, 64 or 32) 16-bit
@@ -546,33 +570,78 @@ __device__ __forceinline__ float norm_cdf(float x, float& ez2) {
   const float c = 0.5f * erfc_nonneg(fabsf(x) * 0.70710678118654752f, ez2);
   return x >= 0.f ? 1.0f - c : c;
 }
-// Stores 8 consecutive 16-bit outputs `v` (already rounded) at element
-// offset `o` of the tile's output rows, applying the epilogue:
-//   kEpiGelu:     out = gelu(v), out2 = gelu'(v)   (v = h, not stored)
-//   kEpiGeluGrad: out = v * aux                    (v = dA, aux = gelu'(h))
-template <typename T, int EPI>
-__device__ __forceinline__ void epilogue8(uint4 v, const TileJob& j, int64_t o) {
+// gelu and gelu' of the two 16-bit values of `w` through the erfc fit.
+template <typename T>
+__device__ __forceinline__ void gelu2_formula(uint32_t w, uint32_t& r, uint32_t& r2) {
+  const float x0 = elem<T>::load((uint16_t)(w & 0xffffu));
+  const float x1 = elem<T>::load((uint16_t)(w >> 16));
+  float e0, e1;
+  const float c0 = norm_cdf(x0, e0), c1 = norm_cdf(x1, e1);
+  r = pack2<T>(x0 * c0, x1 * c1);
+  r2 = pack2<T>(fmaf(x0, e0 * 0.39894228040143268f, c0), fmaf(x1, e1 * 0.39894228040143268f, c1));
+}
+
+// gelu and gelu' of 8 bf16 values: one LDS read each from the generated
+// table (kGeluTab, correctly rounded for 2^-16 <= |x| < 8); the rare values
+// outside that range take the erfc fit.
+__device__ __forceinline__ void gelu8_table(const uint32_t (&w)[4], const uint32_t* tab,
+                                            uint32_t (&r)[4], uint32_t (&r2)[4]) {
+  uint32_t a[8], t[8];
+  bool out = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t e = (i & 1) ? w[i / 2] >> 16 : w[i / 2] & 0xffffu;
+    a[i] = (e & 0x7fffu) - kGeluTabLo;  // wraps to a large value below the range
+    out |= a[i] >= kGeluTabN;
+    t[i] = tab[2 * min(a[i], kGeluTabN - 1) + (e >> 15)];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    r[q] = (t[2 * q] & 0xffffu) | (t[2 * q + 1] << 16);
+    r2[q] = (t[2 * q] >> 16) | (t[2 * q + 1] & 0xffff0000u);
+  }
+  if (out) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool o0 = a[2 * q] >= kGeluTabN, o1 = a[2 * q + 1] >= kGeluTabN;
+      if (o0 || o1) {
+        uint32_t f, f2;
+        gelu2_formula<bf16>(w[q], f, f2);
+        const uint32_t keep = (o0 ? 0u : 0xffffu) | (o1 ? 0u : 0xffff0000u);
+        r[q] = (r[q] & keep) | (f & ~keep);
+        r2[q] = (r2[q] & keep) | (f2 & ~keep);
+      }
+    }
+  }
+}
+
+// Stores 8 consecutive 16-bit outputs `v` (already rounded) at byte offset
+// `off` of the tile's output (descriptor `ro`; `ro2` for the second GELU
+// output), applying the epilogue:
+//   kEpiGelu:     out = gelu(v), out2 = gelu'(v)   (v = h, not stored;
+//                 through `tab` when TAB, else the erfc fit)
+//   kEpiGeluGrad: out = v * gv                     (v = dA, gv = gelu'(h),
+//                 loaded by the caller ahead of time)
+template <typename T, int EPI, bool TAB>
+__device__ __forceinline__ void epilogue8(uint4 v, __amdgpu_buffer_rsrc_t ro,
+                                          __amdgpu_buffer_rsrc_t ro2, uint32_t off, uint4 gv,
+                                          const uint32_t* tab) {
   if (EPI == kEpiPlain) {
-    *reinterpret_cast<uint4*>(j.po + o) = v;
+    store16(ro, off, v);
     return;
   }
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   uint32_t r[4], r2[4];
   if (EPI == kEpiGelu) {
+    if constexpr (TAB) {
+      gelu8_table(w, tab, r, r2);
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float x0 = elem<T>::load((uint16_t)(w[q] & 0xffffu));
-      const float x1 = elem<T>::load((uint16_t)(w[q] >> 16));
-      float e0, e1;
-      const float c0 = norm_cdf(x0, e0), c1 = norm_cdf(x1, e1);
-      r[q] = pack2<T>(x0 * c0, x1 * c1);
-      r2[q] = pack2<T>(fmaf(x0, e0 * 0.39894228040143268f, c0),
-                       fmaf(x1, e1 * 0.39894228040143268f, c1));
+      for (int q = 0; q < 4; ++q) gelu2_formula<T>(w[q], r[q], r2[q]);
     }
-    *reinterpret_cast<uint4*>(j.po + o) = make_uint4(r[0], r[1], r[2], r[3]);
-    *reinterpret_cast<uint4*>(j.po2 + o) = make_uint4(r2[0], r2[1], r2[2], r2[3]);
+    store16(ro, off, make_uint4(r[0], r[1], r[2], r[3]));
+    store16(ro2, off, make_uint4(r2[0], r2[1], r2[2], r2[3]));
   } else {
-    const uint4 gv = *reinterpret_cast<const uint4*>(j.paux + o);
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -582,7 +651,7 @@ __device__ __forceinline__ void epilogue8(uint4 v, const TileJob& j, int64_t o) 
       const float g1 = elem<T>::load((uint16_t)(gw[q] >> 16));
       r[q] = pack2<T>(d0 * g0, d1 * g1);
     }
-    *reinterpret_cast<uint4*>(j.po + o) = make_uint4(r[0], r[1], r[2], r[3]);
+    store16(ro, off, make_uint4(r[0], r[1], r[2], r[3]));
   }
 }
 
@@ -599,15 +668,43 @@ template <int TN>
 constexpr int epi_pitch() { return 64 * TN + 8; }
 template <int TN, int ROWS>
 constexpr int epi_bytes() { return ROWS * epi_pitch<TN>(); }
-template <typename T, int EPI, int ROWS, int TM, int TN>
+// Store instructions one wave issues in store_tile_lds.
+template <int EPI, int ROWS, int TM, int TN>
+constexpr int epi_stores() {
+  return TM * (32 / ROWS) * (ROWS / (64 / (TN * 4))) * (EPI == kEpiGelu ? 2 : 1);
+}
+template <typename T, int EPI, bool TAB, int ROWS, int TM, int TN>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
-                                               int m0, int n0, int lane, char* scratch) {
+                                               int m0, int n0, int lane, char* scratch,
+                                               const uint32_t* tab) {
   static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
   static_assert(ROWS == 32 || ROWS == 16, "32 or 16 scratch rows");
   constexpr int kPitch = epi_pitch<TN>();
   constexpr int kPasses = 32 / ROWS;
   constexpr int kLanesPerRow = TN * 4;       // 16-byte chunks per row
   constexpr int kRowsPerRead = 64 / kLanesPerRow;
+  constexpr int kReads = kPasses * (ROWS / kRowsPerRead);  // 16-byte chunks per lane per sub-tile
+  // kEpiGeluGrad: the gelu'(h) chunk that a lane needs for chunk c of
+  // sub-tile i+1 is loaded as soon as chunk c of sub-tile i is stored, so
+  // its latency hides behind the rest of sub-tile i (kReads chunks in flight,
+  // 4 registers each).
+  uint4 aux[kReads];
+  auto load_aux = [&](int i, int ps, int q) {
+    const int m = m0 + i * 32 + ps * ROWS + q * kRowsPerRead + lane / kLanesPerRow;
+    const int n = n0 + (lane % kLanesPerRow) * 8;
+    uint4 g = make_uint4(0u, 0u, 0u, 0u);
+    if (m < j.rows_valid && n < j.cols_valid)
+      g = *reinterpret_cast<const uint4*>(j.paux + (int64_t)m * j.ldo + n);
+    aux[ps * (ROWS / kRowsPerRead) + q] = g;
+  };
+  if constexpr (EPI == kEpiGeluGrad) {
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps)
+#pragma unroll
+      for (int q = 0; q < ROWS / kRowsPerRead; ++q) load_aux(0, ps, q);
+  }
+  const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
+  const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(EPI == kEpiGelu ? j.po2 : j.po);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -633,7 +730,13 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
         const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kPitch + ch * 16);
         const int m = m0 + i * 32 + ps * ROWS + rr;
         const int n = n0 + ch * 8;
-        if (m < j.rows_valid && n < j.cols_valid) epilogue8<T, EPI>(v, j, (int64_t)m * j.ldo + n);
+        const uint32_t off = (m < j.rows_valid && n < j.cols_valid)
+                                 ? (uint32_t)(((int64_t)m * j.ldo + n) * 2)
+                                 : kOob;
+        epilogue8<T, EPI, TAB>(v, ro, ro2, off, aux[ps * (ROWS / kRowsPerRead) + q], tab);
+        if constexpr (EPI == kEpiGeluGrad) {
+          if (i + 1 < TM) load_aux(i + 1, ps, q);
+        }
       }
     }
   }
@@ -701,6 +804,11 @@ gg_mfma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
   // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
   __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
+  // bf16 GELU epilogue of the 256-row tiles: the gelu / gelu' table in LDS
+  // (the 128-row tiles run two workgroups per CU, which the table would not
+  // leave room for).
+  constexpr bool kTab = EPI == kEpiGelu && std::is_same<T, bf16>::value && BM == 256;
+  __shared__ uint32_t s_gtab[kTab ? kGeluTabWords : 1];
 
   int64_t mtiles;
   if (MODE != kDw) {
@@ -724,6 +832,11 @@ gg_mfma_kernel(GemmArgs g) {
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wm = wave / WGN, wn = wave % WGN;
+  if constexpr (kTab) {
+    // Published by the barrier of the first k-step (or the one before the
+    // first epilogue).
+    for (int i = threadIdx.x; i < kGeluTabWords; i += NW * kWave) s_gtab[i] = kGeluTab[i];
+  }
   FragReader<BM, kAK, TM, BK> fa;
   FragReader<BN, kBKm, TN, BK> fb;
   fa.init(wm * WM, lane);
@@ -767,6 +880,14 @@ gg_mfma_kernel(GemmArgs g) {
     }
   };
 
+  // The LDS-staged epilogue issues kStores store instructions per wave after
+  // the next tile's first stages; the first wait of that tile lets them stay
+  // in flight.
+  constexpr bool kLdsEpi = TN == 2 || TN == 4;
+  constexpr int kRows = !kLdsEpi || NW * epi_bytes<TN, 32>() <= kStage ? 32 : 16;
+  constexpr int kStores = kLdsEpi ? epi_stores<EPI, kRows, TM, TN>() : 0;
+  static_assert((NS - 2) * kLoadsPerStage + kStores < 64, "vmcnt range");
+  bool stores_out = false;
   while (true) {
     zero_acc<T>(acc);
     // Ring pipeline. Iteration kt waits until its own stage has landed (the
@@ -777,7 +898,17 @@ gg_mfma_kernel(GemmArgs g) {
     int slot = 0;
     for (int64_t kt = 0; kt < nk; ++kt) {
       const int64_t younger = nk - 1 - kt;  // stages issued after this one (capped below)
-      if (younger >= NS - 2) {
+      if (kt == 0 && stores_out) {
+        if (younger >= NS - 2) {
+          wait_vmcnt<(NS - 2) * kLoadsPerStage + kStores>();
+        } else if (NS > 3 && younger == 2) {
+          wait_vmcnt<(NS > 3 ? 2 : 0) * kLoadsPerStage + kStores>();
+        } else if (NS > 2 && younger == 1) {
+          wait_vmcnt<(NS > 2 ? 1 : 0) * kLoadsPerStage + kStores>();
+        } else {
+          wait_vmcnt<kStores>();
+        }
+      } else if (younger >= NS - 2) {
         wait_vmcnt<(NS - 2) * kLoadsPerStage>();
       } else if (NS > 3 && younger == 2) {
         wait_vmcnt<(NS > 3 ? 2 : 0) * kLoadsPerStage>();
@@ -812,14 +943,16 @@ gg_mfma_kernel(GemmArgs g) {
     }
     static_assert(TN == 2 || TN == 4 || EPI == kEpiPlain,
                   "fused epilogues use the LDS-staged store");
+    stores_out = false;
     if (MODE == kDw && job.pf != nullptr) {
       store_partial(acc, job, wm * WM, wn * WN, lane);
-    } else if constexpr (TN == 2 || TN == 4) {
+    } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
-      constexpr int kRows = NW * epi_bytes<TN, 32>() <= kStage ? 32 : 16;
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
-      store_tile_lds<T, EPI, kRows>(acc, job, wm * WM, wn * WN, lane,
-                                    smem + (NS - 1) * kStage + wave * epi_bytes<TN, kRows>());
+      store_tile_lds<T, EPI, kTab, kRows>(acc, job, wm * WM, wn * WN, lane,
+                                          smem + (NS - 1) * kStage + wave * epi_bytes<TN, kRows>(),
+                                          s_gtab);
+      stores_out = more;
     } else {
       store_tile<T>(acc, job, wm * WM, wn * WN, lane);
     }
@@ -1186,6 +1319,9 @@ int check_gemm(int dtype, int32_t E, int64_t A, int64_t K, int64_t N, const void
   if ((A > 0 && K > 0 && a == nullptr) || (K > 0 && N > 0 && b == nullptr)) return NT_ERR_INVALID_ARG;
   if (out == nullptr && ((A > 0 && (K > 0 || N > 0)) || (K > 0 && N > 0))) return NT_ERR_INVALID_ARG;
   if (A > INT32_MAX) return NT_ERR_TOO_LARGE;
+  // Tile operand and output offsets are 32-bit byte offsets: 256 rows of
+  // the widest operand row must stay below 2 GiB.
+  if (K > (int64_t{1} << 22) - 256 || N > (int64_t{1} << 22) - 256) return NT_ERR_TOO_LARGE;
   return NT_OK;
 }
 

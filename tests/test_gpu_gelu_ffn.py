@@ -151,3 +151,44 @@ def test_gelu_ffn_matches_unfused_gpu(ext, A, d, f, E):
     close(y_f, y_u)
     for p, q in zip(a, b):
         close(p.grad, q.grad)
+
+
+def test_gemm_gelu_table_edges(ext):
+    """The 256-row tiles read gelu / gelu' from a table covering
+    2^-16 <= |h| < 8 and compute the rest: h spans about +-40 here, with exact
+    zeros (all-zero rows) and tiny values (rows scaled by 2^-20). In-range
+    values must equal the double-precision result rounded once; out-of-range
+    values must meet the bf16 tolerance."""
+    E, d, f = 4, 64, 1024
+    counts = [8192] * E
+    A = sum(counts)
+    g_ = torch.Generator().manual_seed(21)
+    X = torch.randn(A, d, generator=g_)
+    X[::7] *= 12.0                  # |h| up to ~40
+    X[3::11] = 0.0                  # h == 0 exactly
+    X[5::13] *= 2.0**-20            # |h| < 2^-16
+    X = X.to(torch.bfloat16)
+    W = (torch.randn(E, d, f, generator=g_) * 0.4).to(torch.bfloat16)
+    off = _offsets(counts)
+    act, act_grad = ext.grouped_gemm_gelu(X.cuda(), off, W.cuda())
+    h = ext.grouped_gemm_kernel(X.cuda(), off, W.cuda())
+    torch.cuda.synchronize()
+    h = h.cpu().double()
+    # double precision with an accurate lower tail (x * ndtr(x); 1 + erf
+    # cancels below about -5 even in double)
+    from scipy.special import ndtr
+
+    hn = h.numpy()
+    cdf = ndtr(hn)
+    pdf = torch.from_numpy(hn).pow(2).mul(-0.5).exp().numpy() / (2 * torch.pi) ** 0.5
+    want = torch.from_numpy(hn * cdf).to(torch.bfloat16)
+    want_g = torch.from_numpy(cdf + hn * pdf).to(torch.bfloat16)
+    a, ag = act.cpu(), act_grad.cpu()
+    inr = (h.abs() >= 2.0**-16) & (h.abs() < 8.0)
+    assert inr.float().mean() > 0.5 and (~inr).sum() > 1000 and (h == 0).sum() > 1000
+    assert torch.equal(a[inr], want[inr])
+    assert torch.equal(ag[inr], want_g[inr])
+    torch.testing.assert_close(a.double(), want.double(), **TOL[torch.bfloat16])
+    torch.testing.assert_close(ag.double(), want_g.double(), **TOL[torch.bfloat16])
+    assert torch.equal(a[h == 0], torch.zeros_like(a[h == 0]))
+    assert torch.all(ag[h == 0] == 0.5)
