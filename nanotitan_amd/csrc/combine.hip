@@ -23,6 +23,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxSorted = 256;
+// Tokens per wave of the small-fan-in inverse-map kernels (measured at
+// d = 512, k = 2: one for the combine, two for the pack backward; one at
+// k <= 8).
+constexpr int kCombineU = 1;
+constexpr int kPackBwdU = 2;
+constexpr int fan_u(int kmax, int u) { return kmax <= 2 ? u : 1; }
 
 template <typename S, int N>
 struct alignas(sizeof(S) * N) vpack {
@@ -351,6 +357,86 @@ combine_kernel(const typename elem<T>::storage* __restrict__ y, ListSrc src,
   }
 }
 
+// Inverse-map form for small fan-in (k <= KMAX): a wave serves U tokens
+// at once. Each token's k slots are loaded by one segment of 64/U lanes,
+// broadcast and sorted ascending in registers; then every row load of the U
+// tokens is issued before the ordered accumulation, so a wave keeps U * k
+// row loads in flight. Same arithmetic and order as combine_kernel.
+template <int KMAX, int U>
+__device__ __forceinline__ void sorted_slots(const int32_t* __restrict__ inv, int64_t t0,
+                                             int64_t T_, int32_t k, int32_t& mine,
+                                             int32_t (&p)[U][KMAX], int (&n)[U]) {
+  constexpr int kSeg = kWave / U;
+  static_assert(KMAX <= kSeg, "a token's slots fit its lane segment");
+  const int lane = lane_id();
+  const int64_t rows = T_ * k;
+  const int64_t tl = t0 + lane / kSeg;
+  const int jl = lane % kSeg;
+  mine = (jl < k && tl < T_) ? inv[tl * k + jl] : -1;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    n[u] = 0;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      const int32_t v = __shfl(mine, u * kSeg + j, kWave);
+      const bool ok = j < k && v >= 0 && v < rows;
+      p[u][j] = ok ? v : INT32_MAX;
+      n[u] += ok;
+    }
+#pragma unroll
+    for (int i = 0; i < KMAX - 1; ++i)
+#pragma unroll
+      for (int j = 0; j < KMAX - 1 - i; ++j) {
+        const int32_t a = p[u][j], b = p[u][j + 1];
+        p[u][j] = a < b ? a : b;
+        p[u][j + 1] = a < b ? b : a;
+      }
+  }
+}
+
+template <typename T, typename TO, int VE, int KMAX, int U>
+__global__ void __launch_bounds__(kThreads)
+combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
+                   const int32_t* __restrict__ inv, int32_t k, const float* __restrict__ w,
+                   int64_t T_, int64_t d, typename elem<TO>::storage* __restrict__ out) {
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t t0 = ((int64_t)blockIdx.x * kWaves + wave) * U;
+  if (t0 >= T_) return;
+  int32_t mine, p[U][KMAX];
+  int n[U];
+  sorted_slots<KMAX, U>(inv, t0, T_, k, mine, p, n);
+  float wp[U][KMAX];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) wp[u][j] = j < n[u] ? w[p[u][j]] : 0.f;
+  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+    float x[U][KMAX][VE];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j < n[u]) load_vec<T, VE>(y + (int64_t)p[u][j] * d + h, x[u][j]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t0 + u >= T_) break;
+      float acc[VE];
+#pragma unroll
+      for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+      {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+          if (j < n[u])
+#pragma unroll
+            for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp[u][j] * x[u][j][v];
+      }
+      store_vec<TO, VE>(out + (t0 + u) * d + h, acc);
+    }
+  }
+}
+
 // ------------------------------------------------------------- combine bwd
 
 // Generic form, one wave per packed row p:
@@ -499,6 +585,52 @@ pack_bwd_kernel(const typename elem<T>::storage* __restrict__ dpX, const float* 
   }
 }
 
+// Inverse-map pack backward for small fan-in: same sums as pack_bwd_kernel
+// (ascending packed order, fp32), U tokens per wave with every row load
+// issued up front.
+template <typename T, int VE, int KMAX, int U>
+__global__ void __launch_bounds__(kThreads)
+pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
+                    const float* __restrict__ dpw, const int32_t* __restrict__ inv,
+                    int64_t T_, int32_t k, int64_t d, typename elem<T>::storage* __restrict__ dX,
+                    float* __restrict__ dw) {
+  constexpr int kSeg = kWave / U;
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t t0 = ((int64_t)blockIdx.x * kWaves + wave) * U;
+  if (t0 >= T_) return;
+  const int64_t rows = T_ * k;
+  int32_t mine, p[U][KMAX];
+  int n[U];
+  sorted_slots<KMAX, U>(inv, t0, T_, k, mine, p, n);
+  {
+    const int64_t tl = t0 + lane / kSeg;
+    const int jl = lane % kSeg;
+    if (jl < k && tl < T_) dw[tl * k + jl] = (mine >= 0 && mine < rows) ? dpw[mine] : 0.f;
+  }
+  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
+    float x[U][KMAX][VE];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j < n[u]) load_vec<T, VE>(dpX + (int64_t)p[u][j] * d + h, x[u][j]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t0 + u >= T_) break;
+      float acc[VE];
+#pragma unroll
+      for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j < n[u])
+#pragma unroll
+          for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], x[u][j][v]);
+      store_vec<T, VE>(dX + (t0 + u) * d + h, acc);
+    }
+  }
+}
+
 // ------------------------------------------------------------- dispatchers
 
 template <typename T>
@@ -523,6 +655,25 @@ int run_combine(const void* y, ListSrc src, const float* w, int64_t T_, int64_t 
   const int ve = std::min(vec_width<T>(d, y, y, y), vec_width<TO>(d, out, out, out));
   const S* yp = static_cast<const S*>(y);
   SO* op = static_cast<SO*>(out);
+  if (src.start == nullptr && src.k <= 8) {
+#define NT_CI(VE, KM) \
+  hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op)
+#define NT_CI_VE(KM)            \
+  switch (ve) {                 \
+    case 8: NT_CI(8, KM); break; \
+    case 4: NT_CI(4, KM); break; \
+    case 2: NT_CI(2, KM); break; \
+    default: NT_CI(1, KM); break; \
+  }
+    if (src.k <= 2) {
+      NT_CI_VE(2)
+    } else {
+      NT_CI_VE(8)
+    }
+#undef NT_CI_VE
+#undef NT_CI
+    return launch_status();
+  }
   switch (ve) {
     case 8: hipLaunchKernelGGL((combine_kernel<T, TO, 8>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
     case 4: hipLaunchKernelGGL((combine_kernel<T, TO, 4>), grid, dim3(kThreads), 0, s, yp, src, w, T_, d, op); break;
@@ -617,6 +768,25 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   const int ve = vec_width<T>(d, dpX, dX, dX);
   const S* ip = static_cast<const S*>(dpX);
   S* op = static_cast<S*>(dX);
+  if (src.start == nullptr && expert == nullptr && k <= 8) {
+#define NT_PBI(VE, KM) \
+  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, kPackBwdU)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kPackBwdU))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
+#define NT_PBI_VE(KM)            \
+  switch (ve) {                  \
+    case 8: NT_PBI(8, KM); break; \
+    case 4: NT_PBI(4, KM); break; \
+    case 2: NT_PBI(2, KM); break; \
+    default: NT_PBI(1, KM); break; \
+  }
+    if (k <= 2) {
+      NT_PBI_VE(2)
+    } else {
+      NT_PBI_VE(8)
+    }
+#undef NT_PBI_VE
+#undef NT_PBI
+    return launch_status();
+  }
   switch (ve) {
     case 8: hipLaunchKernelGGL((pack_bwd_kernel<T, 8>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;
     case 4: hipLaunchKernelGGL((pack_bwd_kernel<T, 4>), grid, dim3(kThreads), 0, s, ip, dpw, src, expert, topk, T_, k, d, op, dw); break;

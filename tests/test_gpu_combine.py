@@ -156,3 +156,48 @@ def test_combine_rejects_non_fp32_grad(ext):
     with pytest.raises(RuntimeError, match="float32"):
         ext.combine_kernel_backward(y, tid, w, torch.zeros(1, 2, device="cuda",
                                                            dtype=torch.float16), 2)
+
+
+@pytest.mark.parametrize("k", [1, 2, 5, 8, 12])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_inverse_map_kernels_with_dropped_slots(ext, k, dtype):
+    """combine_inv / combine_backward_inv / pack_backward_inv on an inverse
+    map with dropped (-1) and out-of-range slots, slots in random packed
+    order, an odd token count, and k on both sides of the small-fan-in
+    kernels' limit (8): bit-equal to the oracle's token-id forms."""
+    T, d = 301, 40
+    A = T * k
+    g = torch.Generator().manual_seed(100 + k)
+    perm = torch.randperm(A, generator=g).to(torch.int32)
+    inv = perm.view(T, k).clone()
+    drop = torch.rand(T, k, generator=g) < 0.07
+    inv[drop] = -1
+    inv[torch.rand(T, k, generator=g) < 0.02] = A + 5  # out of range: skipped
+    token_id = torch.full((A,), -1, dtype=torch.int32)
+    slot = torch.zeros(A, dtype=torch.int32)
+    for t in range(T):
+        for j in range(k):
+            p = int(inv[t, j])
+            if 0 <= p < A:
+                token_id[p] = t
+                slot[p] = j
+    y = torch.randn(A, d, generator=g).to(dtype)
+    w = torch.randn(A, generator=g)
+    out = ext.combine_inv(y.cuda(), inv.cuda(), w.cuda(), torch.float32)
+    want = O.combine_tokens(y, token_id, w, T)
+    assert torch.equal(bits(out), bits(torch.from_numpy(want)))
+
+    dY = torch.randn(T, d, generator=g)
+    dy, dw = ext.combine_backward_inv(y.cuda(), inv.cuda(), w.cuda(), dY.cuda())
+    want_dy, want_dw = O.combine_backward(y, token_id, w, dY, out_dtype=dtype)
+    valid = (token_id >= 0).numpy()
+    assert torch.equal(bits(dy.cpu()[valid]), bits(want_dy[valid]))
+    np.testing.assert_allclose(dw.cpu().numpy()[valid], want_dw[valid], **DW_TOL)
+
+    dpX = torch.randn(A, d, generator=g).to(dtype)
+    dpw = torch.randn(A, generator=g)
+    topk = torch.arange(k, dtype=torch.int32).repeat(T, 1)  # slot j <-> "expert" j
+    want_dX, want_dw2 = O.pack_backward(dpX, dpw, token_id, slot, topk, out_dtype=dtype)
+    dX, dw2 = ext.pack_backward_inv(dpX.cuda(), dpw.cuda(), inv.cuda())
+    assert torch.equal(bits(dX), bits(want_dX))
+    assert torch.equal(bits(dw2), bits(torch.from_numpy(want_dw2)))
