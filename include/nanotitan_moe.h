@@ -220,6 +220,42 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
                             const void* act_grad, int32_t E, int64_t A, int64_t K, int64_t N,
                             void* dH, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* SwiGLU up-projection: the gate and value GEMMs of each output tile run
+ * in one kernel (the B tiles of W_gate and W_val side by side) and the
+ * epilogue writes gate = X_e @ W_gate[e], value = X_e @ W_val[e] (each
+ * rounded to dtype) and hidden = silu(gate) * value (silu rounded, then the
+ * product rounded), all [A,N]; gate and value are what the backward needs.
+ * W_gate, W_val [E,K,N]. Replaces the two grouped_gemm_kernel calls and the
+ * activation of the reference's SwiGLU ExpertFFN
+ * (src/model/feed_fwd.py:107-110). */
+int nt_grouped_gemm_swiglu(int dtype, const void* X, const int32_t* offsets, const void* W_gate,
+                           const void* W_val, int32_t E, int64_t A, int64_t K, int64_t N,
+                           void* hidden, void* gate, void* value, void* ws, size_t ws_bytes,
+                           hipStream_t stream);
+
+/* dX GEMM with the SwiGLU backward in its epilogue: with
+ * dhidden = dOut @ W[e]^T rounded to dtype, writes
+ * dvalue = dhidden * silu(gate) and dgate = (dhidden * value) * silu'(gate)
+ * (each product rounded where torch's autograd of silu(gate) * value
+ * rounds it). W [E,K,N] (W_out), dOut [A,N], gate / value / dgate / dvalue
+ * [A,K]. Replaces bwd_grouped_gemm_dX_kernel followed by the autograd of
+ * the activation (reference csrc/kernels/bwd_grouped_gemm_dX.cu:46-96,
+ * src/model/feed_fwd.py:110). */
+int nt_grouped_gemm_dx_swiglu(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                              const void* gate, const void* value, int32_t E, int64_t A,
+                              int64_t K, int64_t N, void* dgate, void* dvalue, void* ws,
+                              size_t ws_bytes, hipStream_t stream);
+
+/* Two dX products summed in one GEMM over the concatenated reduction:
+ * dX[a,:] = dOut1[a,:] @ W1[e]^T + dOut2[a,:] @ W2[e]^T, fp32 accumulation,
+ * one rounding. W1, W2 [E,K,N], dOut1, dOut2 [A,N], dX [A,K]. Replaces the
+ * two bwd_grouped_gemm_dX_kernel calls of the SwiGLU gate and value
+ * projections and the autograd sum of their results
+ * (reference csrc/kernels/bwd_grouped_gemm_dX.cu:46-96, src/model/feed_fwd.py:108-109). */
+int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t* offsets,
+                        const void* dOut1, const void* dOut2, int32_t E, int64_t A, int64_t K,
+                        int64_t N, void* dX, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* dW[e] = X_e^T @ dOut_e summed over the rows of expert e (zero for an empty
  * expert). X [A,K], dOut [A,N], dW [E,K,N]. An expert with more rows than a
  * chunk (at least twice the mean expert size) is reduced in chunks whose

@@ -371,11 +371,30 @@ struct GemmArgs {
   const void* aux;  // fused GELU backward: gelu'(h), same layout as out
   int32_t chunk;    // dW: rows per reduction chunk (0: one chunk per expert)
   float* partial;   // dW: fp32 partial slabs [split chunks][K][N] when chunk > 0
+  // SwiGLU forward: b2 = W_val (b = W_gate), out = hidden, out2 = gate,
+  // out3 = value. SwiGLU backward: aux = gate, aux2 = value, out = dgate,
+  // out2 = dvalue. Two-part dX: a2 / b2 = dOut / W of the second product.
+  const void* a2;
+  const void* b2;
+  void* out3;
+  const void* aux2;
 };
 
 // Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
-// itself is not stored); backward GELU (out = C * aux, aux = gelu'(h)).
-enum GemmEpilogue { kEpiPlain = 0, kEpiGelu = 1, kEpiGeluGrad = 2 };
+// itself is not stored); backward GELU (out = C * aux, aux = gelu'(h));
+// SwiGLU forward (gate and value tiles of one output tile computed side by
+// side: out = silu(gate) * value, out2 = gate, out3 = value); SwiGLU
+// backward (C = dhidden: out = dgate, out2 = dvalue from aux = gate, aux2 =
+// value); two-part dX (plain store, C = dOut @ W^T + dOut2 @ W2^T over one
+// concatenated reduction).
+enum GemmEpilogue {
+  kEpiPlain = 0,
+  kEpiGelu = 1,
+  kEpiGeluGrad = 2,
+  kEpiSwiGLU = 3,
+  kEpiSwiGLUGrad = 4,
+  kEpiDualK = 5
+};
 
 // Logical tile -> (m-tile, n-tile): groups of kGroupM m-tiles, m fastest
 // inside a group, so neighbouring logical tiles reuse both A and B panels.
@@ -400,19 +419,31 @@ struct TileJob {
   int64_t kred;                    // reduction length
   uint16_t* po;
   int64_t ldo;
-  uint16_t* po2;          // fused GELU forward: gelu'(h) output (or null)
-  const uint16_t* paux;   // fused GELU backward: gelu'(h) input (or null)
+  uint16_t* po2;          // second output (GELU: gelu'(h); SwiGLU: gate / dvalue)
+  uint16_t* po3;          // SwiGLU forward: value output
+  const uint16_t* paux;   // GELU backward: gelu'(h); SwiGLU backward: gate
+  const uint16_t* paux2;  // SwiGLU backward: value
+  const uint16_t* pa2;    // two-part dX: second A operand origin
+  const uint16_t* pb2;    // SwiGLU forward: value weights; two-part dX: second W
+  int64_t kred1;          // two-part dX: reduction length of the first part
   float* pf;              // dW of a split expert: fp32 partial slab origin (or null)
 };
 
 // Operands and extents of logical output tile `logical` (< mtiles * ntn).
 // For the row-tiled modes s_pref must hold the m-tile prefix of the experts
 // (build_m_prefix) and `mtiles` its total.
-template <int MODE, int BM, int BN>
+// SwiGLU forward tiles are BN wide in the MFMA (gate and value halves) and
+// BN / 2 wide in the output.
+template <int MODE, int BM, int BN, int EPI = kEpiPlain>
 __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pref, int64_t mtiles,
                                           int64_t logical, TileJob& j) {
   j.po2 = nullptr;
+  j.po3 = nullptr;
   j.paux = nullptr;
+  j.paux2 = nullptr;
+  j.pa2 = nullptr;
+  j.pb2 = nullptr;
+  j.kred1 = 0;
   j.pf = nullptr;
   int64_t mt;
   int nt;
@@ -458,48 +489,78 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
     const int64_t row0 = r0 + mtl * BM;
     j.rows_valid = r1 - row0;
     if (MODE == kFwd) {
+      constexpr int64_t BNO = EPI == kEpiSwiGLU ? BN / 2 : BN;  // output columns per tile
+      const int64_t wofs = (int64_t)e * g.K * g.N + (int64_t)nt * BNO;
+      const int64_t oofs = row0 * g.N + (int64_t)nt * BNO;
       j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
       j.lda = g.K;
-      j.pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN;
+      j.pb = static_cast<const uint16_t*>(g.b) + wofs;
       j.ldb = g.N;
-      j.cols_valid = g.N - (int64_t)nt * BN;
+      j.cols_valid = g.N - (int64_t)nt * BNO;
       j.kred = g.K;
-      j.po = static_cast<uint16_t*>(g.out) + row0 * g.N + (int64_t)nt * BN;
+      j.po = static_cast<uint16_t*>(g.out) + oofs;
       j.ldo = g.N;
-      if (g.out2) j.po2 = static_cast<uint16_t*>(g.out2) + row0 * g.N + (int64_t)nt * BN;
+      if (g.out2) j.po2 = static_cast<uint16_t*>(g.out2) + oofs;
+      if (EPI == kEpiSwiGLU) {
+        j.pb2 = static_cast<const uint16_t*>(g.b2) + wofs;
+        j.po3 = static_cast<uint16_t*>(g.out3) + oofs;
+      }
     } else {  // kDx
+      const int64_t oofs = row0 * g.K + (int64_t)nt * BN;
       j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
       j.lda = g.N;
       j.pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
       j.ldb = g.N;
       j.cols_valid = g.K - (int64_t)nt * BN;
       j.kred = g.N;
-      j.po = static_cast<uint16_t*>(g.out) + row0 * g.K + (int64_t)nt * BN;
+      j.po = static_cast<uint16_t*>(g.out) + oofs;
       j.ldo = g.K;
-      if (g.aux) j.paux = static_cast<const uint16_t*>(g.aux) + row0 * g.K + (int64_t)nt * BN;
+      if (g.aux) j.paux = static_cast<const uint16_t*>(g.aux) + oofs;
+      if (EPI == kEpiSwiGLUGrad) {
+        j.paux2 = static_cast<const uint16_t*>(g.aux2) + oofs;
+        j.po2 = static_cast<uint16_t*>(g.out2) + oofs;
+      }
+      if (EPI == kEpiDualK) {
+        j.pa2 = static_cast<const uint16_t*>(g.a2) + row0 * g.N;
+        j.pb2 = static_cast<const uint16_t*>(g.b2) + (int64_t)e * g.K * g.N +
+                (int64_t)nt * BN * g.N;
+        j.kred1 = g.N;
+        j.kred = 2 * g.N;
+      }
     }
   }
 }
 
 // Global loads of one k-step of both operands of a tile into an LDS stage.
-template <int BM, int BN, bool AK, bool BKM, int BK, int NW>
+// DUAL 1 (SwiGLU forward): the B tile is two BN/2-column halves, gate
+// weights then value weights, for the same output columns. DUAL 2 (two-part
+// dX): k-steps below kred1 / BK read (pa, pb), the rest (pa2, pb2).
+template <int BM, int BN, bool AK, bool BKM, int BK, int NW, int DUAL = 0>
 struct StageLoader {
   typedef OperandTile<BM, AK, BK, NW> TA;
-  typedef OperandTile<BN, BKM, BK, NW> TB;
+  typedef OperandTile<DUAL == 1 ? BN / 2 : BN, BKM, BK, NW> TB;
+  static constexpr int kBBytes = (DUAL == 1 ? 2 : 1) * TB::kBytes;
+  static constexpr int kLoads = TA::kPer + (DUAL == 1 ? 2 : 1) * TB::kPer;  // per wave
   TA ta;
   TB tb;
   const uint16_t* pa;
   const uint16_t* pb;
-  int64_t lda, ldb, rv, cv, kred;
+  const uint16_t* pa2;
+  const uint16_t* pb2;
+  int64_t lda, ldb, rv, cv, kred, kred1;
   int wave;
   __device__ void init(const TileJob& j, int wave_, int lane) {
+    constexpr int kCols = DUAL == 1 ? BN / 2 : BN;
     pa = j.pa;
     pb = j.pb;
+    pa2 = j.pa2;
+    pb2 = j.pb2;
     lda = j.lda;
     ldb = j.ldb;
     rv = j.rows_valid < BM ? j.rows_valid : BM;
-    cv = j.cols_valid < BN ? j.cols_valid : BN;
+    cv = j.cols_valid < kCols ? j.cols_valid : kCols;
     kred = j.kred;
+    kred1 = j.kred1;
     wave = wave_;
     ta.init(lda, wave, lane);
     tb.init(ldb, wave, lane);
@@ -507,13 +568,26 @@ struct StageLoader {
   // Issue this wave's loads of k-step kt into the stage at `lds` (A tile
   // first, then the B tile).
   __device__ void issue(int64_t kt, char* lds) const {
-    const int64_t kleft = kred - kt * BK;
+    const uint16_t* a = pa;
+    const uint16_t* b = pb;
+    int64_t kl = kt * BK, klen = kred;
+    if (DUAL == 2) {
+      klen = kred1;
+      if (kl >= kred1) {
+        a = pa2;
+        b = pb2;
+        kl -= kred1;
+        klen = kred - kred1;
+      }
+    }
+    const int64_t kleft = klen - kl;
     const int64_t kv = kleft < BK ? kleft : BK;
     // Readable bytes from each tile origin: up to the last valid element.
     const int64_t ra = AK ? ((rv - 1) * lda + kv) * 2 : ((kv - 1) * lda + rv) * 2;
     const int64_t rb = BKM ? ((cv - 1) * ldb + kv) * 2 : ((kv - 1) * ldb + cv) * 2;
-    ta.issue(pa + kt * (AK ? BK : BK * lda), ra, lds, kv, wave);
-    tb.issue(pb + kt * (BKM ? BK : BK * ldb), rb, lds + TA::kBytes, kv, wave);
+    ta.issue(a + (AK ? kl : kl * lda), ra, lds, kv, wave);
+    tb.issue(b + (BKM ? kl : kl * ldb), rb, lds + TA::kBytes, kv, wave);
+    if (DUAL == 1) tb.issue(pb2 + (BKM ? kl : kl * ldb), rb, lds + TA::kBytes + TB::kBytes, kv, wave);
   }
 };
 
@@ -615,6 +689,31 @@ __device__ __forceinline__ void gelu8_table(const uint32_t (&w)[4], const uint32
   }
 }
 
+// SwiGLU pieces in fp32, in the order torch evaluates silu and its
+// backward: silu(x) = x * sigma(x), silu'(x) = sigma(x) (1 + x (1 - sigma(x))),
+// sigma(x) = 1 / (1 + e^-x). Every tensor the reference's unfused graph
+// stores is rounded to T where it would be (round<T>).
+template <typename T>
+__device__ __forceinline__ float round_to(float x) {
+  return elem<T>::load(elem<T>::store(x));
+}
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+// hidden = round(round(silu(g)) * v) for rounded g, v.
+template <typename T>
+__device__ __forceinline__ float swiglu_hidden(float g, float v) {
+  return round_to<T>(round_to<T>(g * sigmoid_f(g)) * v);
+}
+// dgate, dvalue from rounded dhidden, gate, value.
+template <typename T>
+__device__ __forceinline__ void swiglu_grad(float dh, float g, float v, float& dg, float& dv) {
+  const float sg = sigmoid_f(g);
+  dv = round_to<T>(dh * round_to<T>(g * sg));
+  const float ds = round_to<T>(dh * v);
+  dg = round_to<T>((ds * sg) * (1.0f + g * (1.0f - sg)));
+}
+
 // Stores 8 consecutive 16-bit outputs `v` (already rounded) at byte offset
 // `off` of the tile's output (descriptor `ro`; `ro2` for the second GELU
 // output), applying the epilogue:
@@ -622,12 +721,34 @@ __device__ __forceinline__ void gelu8_table(const uint32_t (&w)[4], const uint32
 //                 through `tab` when TAB, else the erfc fit)
 //   kEpiGeluGrad: out = v * gv                     (v = dA, gv = gelu'(h),
 //                 loaded by the caller ahead of time)
+//   kEpiSwiGLUGrad: out = dgate, out2 = dvalue     (v = dhidden, gv = gate,
+//                 gv2 = value)
 template <typename T, int EPI, bool TAB>
 __device__ __forceinline__ void epilogue8(uint4 v, __amdgpu_buffer_rsrc_t ro,
                                           __amdgpu_buffer_rsrc_t ro2, uint32_t off, uint4 gv,
-                                          const uint32_t* tab) {
-  if (EPI == kEpiPlain) {
+                                          uint4 gv2, const uint32_t* tab) {
+  if (EPI == kEpiPlain || EPI == kEpiDualK) {
     store16(ro, off, v);
+    return;
+  }
+  if (EPI == kEpiSwiGLUGrad) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    const uint32_t vw[4] = {gv2.x, gv2.y, gv2.z, gv2.w};
+    uint32_t rg[4], rv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float dg0, dv0, dg1, dv1;
+      swiglu_grad<T>(elem<T>::load((uint16_t)(w[q] & 0xffffu)),
+                     elem<T>::load((uint16_t)(gw[q] & 0xffffu)),
+                     elem<T>::load((uint16_t)(vw[q] & 0xffffu)), dg0, dv0);
+      swiglu_grad<T>(elem<T>::load((uint16_t)(w[q] >> 16)), elem<T>::load((uint16_t)(gw[q] >> 16)),
+                     elem<T>::load((uint16_t)(vw[q] >> 16)), dg1, dv1);
+      rg[q] = pack2<T>(dg0, dg1);
+      rv[q] = pack2<T>(dv0, dv1);
+    }
+    store16(ro, off, make_uint4(rg[0], rg[1], rg[2], rg[3]));
+    store16(ro2, off, make_uint4(rv[0], rv[1], rv[2], rv[3]));
     return;
   }
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -671,7 +792,8 @@ constexpr int epi_bytes() { return ROWS * epi_pitch<TN>(); }
 // Store instructions one wave issues in store_tile_lds.
 template <int EPI, int ROWS, int TM, int TN>
 constexpr int epi_stores() {
-  return TM * (32 / ROWS) * (ROWS / (64 / (TN * 4))) * (EPI == kEpiGelu ? 2 : 1);
+  return TM * (32 / ROWS) * (ROWS / (64 / (TN * 4))) *
+         (EPI == kEpiGelu || EPI == kEpiSwiGLUGrad ? 2 : 1);
 }
 template <typename T, int EPI, bool TAB, int ROWS, int TM, int TN>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
@@ -688,23 +810,30 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
   // sub-tile i+1 is loaded as soon as chunk c of sub-tile i is stored, so
   // its latency hides behind the rest of sub-tile i (kReads chunks in flight,
   // 4 registers each).
-  uint4 aux[kReads];
+  // kEpiSwiGLUGrad loads two inputs (gate and value) the same way.
+  constexpr bool kAux = EPI == kEpiGeluGrad || EPI == kEpiSwiGLUGrad;
+  constexpr bool kAux2 = EPI == kEpiSwiGLUGrad;
+  uint4 aux[kReads], aux2[kReads];
   auto load_aux = [&](int i, int ps, int q) {
     const int m = m0 + i * 32 + ps * ROWS + q * kRowsPerRead + lane / kLanesPerRow;
     const int n = n0 + (lane % kLanesPerRow) * 8;
-    uint4 g = make_uint4(0u, 0u, 0u, 0u);
-    if (m < j.rows_valid && n < j.cols_valid)
+    uint4 g = make_uint4(0u, 0u, 0u, 0u), g2 = g;
+    if (m < j.rows_valid && n < j.cols_valid) {
       g = *reinterpret_cast<const uint4*>(j.paux + (int64_t)m * j.ldo + n);
+      if (kAux2) g2 = *reinterpret_cast<const uint4*>(j.paux2 + (int64_t)m * j.ldo + n);
+    }
     aux[ps * (ROWS / kRowsPerRead) + q] = g;
+    aux2[ps * (ROWS / kRowsPerRead) + q] = g2;
   };
-  if constexpr (EPI == kEpiGeluGrad) {
+  if constexpr (kAux) {
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps)
 #pragma unroll
       for (int q = 0; q < ROWS / kRowsPerRead; ++q) load_aux(0, ps, q);
   }
   const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
-  const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(EPI == kEpiGelu ? j.po2 : j.po);
+  const __amdgpu_buffer_rsrc_t ro2 =
+      out_rsrc(EPI == kEpiGelu || EPI == kEpiSwiGLUGrad ? j.po2 : j.po);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -733,8 +862,9 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
         const uint32_t off = (m < j.rows_valid && n < j.cols_valid)
                                  ? (uint32_t)(((int64_t)m * j.ldo + n) * 2)
                                  : kOob;
-        epilogue8<T, EPI, TAB>(v, ro, ro2, off, aux[ps * (ROWS / kRowsPerRead) + q], tab);
-        if constexpr (EPI == kEpiGeluGrad) {
+        epilogue8<T, EPI, TAB>(v, ro, ro2, off, aux[ps * (ROWS / kRowsPerRead) + q],
+                               aux2[ps * (ROWS / kRowsPerRead) + q], tab);
+        if constexpr (kAux) {
           if (i + 1 < TM) load_aux(i + 1, ps, q);
         }
       }
@@ -798,9 +928,12 @@ gg_mfma_kernel(GemmArgs g) {
   static_assert(NS >= 2, "at least two LDS stages");
   constexpr bool kAK = MODE != kDw;   // A operand K-major?
   constexpr bool kBKm = MODE == kDx;  // B operand K-major?
-  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW> Loader;
-  constexpr int kStage = Loader::TA::kBytes + Loader::TB::kBytes;
-  constexpr int kLoadsPerStage = Loader::TA::kPer + Loader::TB::kPer;  // per wave
+  constexpr int kDual = EPI == kEpiSwiGLU ? 1 : (EPI == kEpiDualK ? 2 : 0);
+  static_assert(kDual != 1 || (MODE == kFwd && TN % 2 == 0), "SwiGLU: forward, gate|value halves");
+  static_assert(kDual != 2 || MODE == kDx, "two-part reduction: dX only");
+  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW, kDual> Loader;
+  constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
+  constexpr int kLoadsPerStage = Loader::kLoads;  // per wave
   __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
   // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
   __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
@@ -837,13 +970,18 @@ gg_mfma_kernel(GemmArgs g) {
     // first epilogue).
     for (int i = threadIdx.x; i < kGeluTabWords; i += NW * kWave) s_gtab[i] = kGeluTab[i];
   }
+  // B fragments: one reader over the BN-column tile, or (SwiGLU) one per
+  // half: sub-tiles j < TN/2 are gate columns, the others the value columns
+  // of the same outputs.
+  constexpr int kBRows = kDual == 1 ? BN / 2 : BN;
+  constexpr int kBTs = kDual == 1 ? TN / 2 : TN;
   FragReader<BM, kAK, TM, BK> fa;
-  FragReader<BN, kBKm, TN, BK> fb;
+  FragReader<kBRows, kBKm, kBTs, BK> fb;
   fa.init(wm * WM, lane);
-  fb.init(wn * WN, lane);
+  fb.init(wn * (WN * kBRows / BN), lane);
 
   TileJob job;
-  setup_job<MODE, BM, BN>(g, s_pref, mtiles, logical, job);
+  setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, logical, job);
   Loader ld;
   ld.init(job, wave, lane);
   int64_t nk = ceil_div(job.kred, BK);
@@ -858,10 +996,15 @@ gg_mfma_kernel(GemmArgs g) {
   // the LDS latency of ks+1 hides behind the MFMAs of ks.
   auto compute = [&](const char* sa, const char* sb) {
     vec av[2][TM], bv[2][TN];
+    auto read_b = [&](int j, int ks) {
+      if (kDual == 1 && j >= kBTs)
+        return fb.template read<vec>(sb + Loader::TB::kBytes, j - kBTs, ks);
+      return fb.template read<vec>(sb, j, ks);
+    };
 #pragma unroll
     for (int i = 0; i < TM; ++i) av[0][i] = fa.template read<vec>(sa, i, 0);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bv[0][j] = fb.template read<vec>(sb, j, 0);
+    for (int j = 0; j < TN; ++j) bv[0][j] = read_b(j, 0);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int cur = ks & 1;
@@ -869,7 +1012,7 @@ gg_mfma_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = fb.template read<vec>(sb, j, ks + 1);
+        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = read_b(j, ks + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -883,9 +1026,14 @@ gg_mfma_kernel(GemmArgs g) {
   // The LDS-staged epilogue issues kStores store instructions per wave after
   // the next tile's first stages; the first wait of that tile lets them stay
   // in flight.
-  constexpr bool kLdsEpi = TN == 2 || TN == 4;
-  constexpr int kRows = !kLdsEpi || NW * epi_bytes<TN, 32>() <= kStage ? 32 : 16;
-  constexpr int kStores = kLdsEpi ? epi_stores<EPI, kRows, TM, TN>() : 0;
+  // SwiGLU stores three outputs of TN/2 sub-tiles each (gate, value, hidden).
+  constexpr int TNO = kDual == 1 ? TN / 2 : TN;
+  constexpr bool kLdsEpi = TNO == 2 || TNO == 4;
+  constexpr int kRows = !kLdsEpi || NW * epi_bytes<TNO, 32>() <= kStage ? 32 : 16;
+  constexpr int kStores =
+      !kLdsEpi ? 0
+               : (kDual == 1 ? 3 * epi_stores<kEpiPlain, kRows, TM, TNO>()
+                             : epi_stores<EPI, kRows, TM, TN>());
   static_assert((NS - 2) * kLoadsPerStage + kStores < 64, "vmcnt range");
   bool stores_out = false;
   while (true) {
@@ -934,18 +1082,52 @@ gg_mfma_kernel(GemmArgs g) {
     __syncthreads();
     TileJob nj;
     if (more) {
-      setup_job<MODE, BM, BN>(g, s_pref, mtiles, next, nj);
+      setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, next, nj);
       ld.init(nj, wave, lane);
       nk = ceil_div(nj.kred, BK);
 #pragma unroll
       for (int s0 = 0; s0 < NS - 1; ++s0)
         if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
     }
-    static_assert(TN == 2 || TN == 4 || EPI == kEpiPlain,
-                  "fused epilogues use the LDS-staged store");
+    static_assert(kLdsEpi || EPI == kEpiPlain, "fused epilogues use the LDS-staged store");
     stores_out = false;
     if (MODE == kDw && job.pf != nullptr) {
       store_partial(acc, job, wm * WM, wn * WN, lane);
+    } else if constexpr (kDual == 1) {
+      // gate and value rounded as the unfused GEMMs would store them, then
+      // hidden = round(round(silu(gate)) * value); three LDS-staged stores.
+      static_assert(NW * epi_bytes<TNO, kRows>() <= kStage, "epilogue scratch fits one stage");
+      char* scr = smem + (NS - 1) * kStage + wave * epi_bytes<TNO, kRows>();
+      const int n0 = wn * (WN / 2);
+      f32x16_t part[TM][TNO];
+      TileJob jo = job;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jn = 0; jn < TNO; ++jn)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            acc[i][jn][v] = round_to<T>(acc[i][jn][v]);
+            acc[i][jn + TNO][v] = round_to<T>(acc[i][jn + TNO][v]);
+            part[i][jn][v] = acc[i][jn][v];
+          }
+      jo.po = job.po2;
+      store_tile_lds<T, kEpiPlain, false, kRows>(part, jo, wm * WM, n0, lane, scr, s_gtab);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jn = 0; jn < TNO; ++jn) part[i][jn] = acc[i][jn + TNO];
+      jo.po = job.po3;
+      store_tile_lds<T, kEpiPlain, false, kRows>(part, jo, wm * WM, n0, lane, scr, s_gtab);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jn = 0; jn < TNO; ++jn)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            part[i][jn][v] = swiglu_hidden<T>(acc[i][jn][v], acc[i][jn + TNO][v]);
+      store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
+      stores_out = more;
     } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
@@ -1005,6 +1187,10 @@ gg_generic_kernel(GemmArgs g) {
   const S* X = static_cast<const S*>(g.a);
   const S* Bm = static_cast<const S*>(g.b);
   S* out = static_cast<S*>(g.out);
+  // Two-part dX: reduction indices N .. 2N-1 read (a2, b2).
+  const bool dual = MODE == kDx && g.a2 != nullptr;
+  const S* X2 = static_cast<const S*>(g.a2);
+  const S* B2 = static_cast<const S*>(g.b2);
   const int64_t bid = blockIdx.x;
   const int nt = (int)(bid % g.ntn);
   const int64_t mt = bid / g.ntn;
@@ -1024,7 +1210,7 @@ gg_generic_kernel(GemmArgs g) {
     m0 = r0 + mtl * kGT;
     rows_valid = r1 - m0;
     cols_valid = (MODE == kFwd ? g.N : g.K) - (int64_t)nt * kGT;
-    kred = MODE == kFwd ? g.K : g.N;
+    kred = MODE == kFwd ? g.K : (dual ? 2 * g.N : g.N);
   }
   const int64_t n0 = (int64_t)nt * kGT;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
@@ -1039,15 +1225,18 @@ gg_generic_kernel(GemmArgs g) {
       const int kk = q / kGT, m = q % kGT;
       const int64_t kg = k0 + kk;
       AT va = 0, vb = 0;
+      const bool second = dual && kg >= g.N;
+      const int64_t kx = second ? kg - g.N : kg;
       if (kg < kred && m < rows_valid) {
         if (MODE == kFwd) va = to_acc<T>(X[(m0 + m) * g.K + kg]);
-        else if (MODE == kDx) va = to_acc<T>(X[(m0 + m) * g.N + kg]);
+        else if (MODE == kDx) va = to_acc<T>((second ? X2 : X)[(m0 + m) * g.N + kx]);
         else va = to_acc<T>(X[(r0 + kg) * g.K + m0 + m]);
       }
       if (kg < kred && m < cols_valid) {
         const int64_t n = n0 + m;
         if (MODE == kFwd) vb = to_acc<T>(Bm[(int64_t)e * g.K * g.N + kg * g.N + n]);
-        else if (MODE == kDx) vb = to_acc<T>(Bm[(int64_t)e * g.K * g.N + n * g.N + kg]);
+        else if (MODE == kDx)
+          vb = to_acc<T>((second ? B2 : Bm)[(int64_t)e * g.K * g.N + n * g.N + kx]);
         else vb = to_acc<T>(Bm[(r0 + kg) * g.N + n]);
       }
       s_a[kk][m] = va;
@@ -1136,7 +1325,7 @@ int blocks_per_cu(K kernel, int threads) {
 
 template <int MODE, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS>
 int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
-  const int64_t tiles = plan_tiles<MODE>(g, out_cols, BM, BN);
+  const int64_t tiles = plan_tiles<MODE>(g, out_cols, BM, EPI == kEpiSwiGLU ? BN / 2 : BN);
   if (tiles == 0) return NT_OK;
   if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
   constexpr int threads = WGM * WGN * kWave;
@@ -1163,9 +1352,16 @@ int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t tiles256 = MODE == kDw
                                ? chunks * ceil_div(g.K, 256) * ceil_div(out_cols, 256)
                                : ceil_div(g.A, 256) * ceil_div(out_cols, 256);
-  if (tiles256 * 2 >= (int64_t)device_cus() * 3)
-    return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
-  return launch_mfma<MODE, EPI, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
+  // SwiGLU forward: 256 rows x (128 gate | 128 value) columns, waves 4 x 2,
+  // so that each wave holds the gate and value tiles of the same outputs.
+  if constexpr (EPI == kEpiSwiGLU) {
+    (void)tiles256;
+    return launch_mfma<MODE, EPI, 256, 256, 4, 2, 64, 2>(dtype, g, out_cols, s);
+  } else {
+    if (tiles256 * 2 >= (int64_t)device_cus() * 3)
+      return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
+    return launch_mfma<MODE, EPI, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
+  }
 }
 
 // Elementwise GELU for the generic path (fp32 / fp64, or shapes the MFMA
@@ -1200,6 +1396,50 @@ int launch_gelu_elementwise(int dtype, void* io, void* g, int64_t n, hipStream_t
     case NT_F64: hipLaunchKernelGGL((gelu_elementwise_kernel<double, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
     case NT_F16: hipLaunchKernelGGL((gelu_elementwise_kernel<f16, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
     case NT_BF16: hipLaunchKernelGGL((gelu_elementwise_kernel<bf16, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
+    default: return NT_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+// Elementwise SwiGLU for the generic path. Forward: h = silu(g) * v from
+// the stored gate and value. Backward: io holds dhidden on entry and
+// dvalue on exit, dg receives dgate. Same roundings as the MFMA epilogues
+// for 16-bit types; fp32 / fp64 keep full precision throughout.
+template <typename T, bool GRAD>
+__global__ void __launch_bounds__(256)
+swiglu_elementwise_kernel(void* io_, void* dg_, const void* g_, const void* v_, int64_t n) {
+  typedef typename elem<T>::storage S;
+  typedef typename acc_type<T>::type AT;
+  S* io = static_cast<S*>(io_);
+  S* dg = static_cast<S*>(dg_);
+  const S* gp = static_cast<const S*>(g_);
+  const S* vp = static_cast<const S*>(v_);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const AT g = to_acc<T>(gp[i]);
+    const AT v = to_acc<T>(vp[i]);
+    const AT sg = AT(1) / (AT(1) + exp(-g));
+    const AT silu = to_acc<T>(from_acc<T>(g * sg));
+    if (GRAD) {
+      const AT dh = to_acc<T>(io[i]);
+      const AT ds = to_acc<T>(from_acc<T>(dh * v));
+      dg[i] = from_acc<T>((ds * sg) * (AT(1) + g * (AT(1) - sg)));
+      io[i] = from_acc<T>(dh * silu);
+    } else {
+      io[i] = from_acc<T>(silu * v);
+    }
+  }
+}
+template <bool GRAD>
+int launch_swiglu_elementwise(int dtype, void* io, void* dg, const void* g, const void* v,
+                              int64_t n, hipStream_t s) {
+  if (n == 0) return NT_OK;
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus() * 16));
+  switch (dtype) {
+    case NT_F32: hipLaunchKernelGGL((swiglu_elementwise_kernel<float, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
+    case NT_F64: hipLaunchKernelGGL((swiglu_elementwise_kernel<double, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
+    case NT_F16: hipLaunchKernelGGL((swiglu_elementwise_kernel<f16, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
+    case NT_BF16: hipLaunchKernelGGL((swiglu_elementwise_kernel<bf16, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
     default: return NT_ERR_DTYPE;
   }
   return launch_status();
@@ -1282,6 +1522,31 @@ size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
 template <int MODE, int EPI>
 int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t s) {
   if (mfma) return launch_mfma_auto<MODE, EPI>(dtype, g, out_cols, s);
+  if constexpr (EPI == kEpiSwiGLU) {
+    // Generic path: the gate and value GEMMs, then the elementwise SwiGLU.
+    GemmArgs gg = g;
+    gg.out = g.out2;
+    gg.out2 = nullptr;
+    int st = launch_mode<MODE, kEpiPlain>(dtype, gg, out_cols, false, s);
+    if (st != NT_OK) return st;
+    gg.b = g.b2;
+    gg.out = g.out3;
+    st = launch_mode<MODE, kEpiPlain>(dtype, gg, out_cols, false, s);
+    if (st != NT_OK) return st;
+    return launch_swiglu_elementwise<false>(dtype, g.out, nullptr, g.out2, g.out3,
+                                            g.A * out_cols, s);
+  }
+  if constexpr (EPI == kEpiSwiGLUGrad) {
+    // Generic path: dhidden into the dvalue buffer, then the elementwise
+    // backward (dgate -> out, dvalue over dhidden).
+    GemmArgs gg = g;
+    gg.out = g.out2;
+    gg.aux = nullptr;
+    int st = launch_mode<MODE, kEpiPlain>(dtype, gg, out_cols, false, s);
+    if (st != NT_OK) return st;
+    return launch_swiglu_elementwise<true>(dtype, g.out2, g.out, g.aux, g.aux2, g.A * out_cols,
+                                           s);
+  }
   g.ntn = (int32_t)ceil_div(out_cols, kGT);
   int64_t nblocks;
   if (MODE == kDw) {
@@ -1302,7 +1567,7 @@ int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t 
     default: return NT_ERR_DTYPE;
   }
   int st = launch_status();
-  if (st != NT_OK || EPI == kEpiPlain) return st;
+  if (st != NT_OK || (EPI != kEpiGelu && EPI != kEpiGeluGrad)) return st;
   // Generic path: the GELU epilogue as a second, elementwise pass over the
   // output rows (rows past offsets[E] hold unspecified values either way).
   const int64_t n = g.A * out_cols;
@@ -1390,6 +1655,61 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
   const bool mfma =
       mfma_ok(dtype, K, N, dOut, W, dH) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
   return launch_mode<kDx, kEpiGeluGrad>(dtype, g, K, mfma, stream);
+}
+
+int nt_grouped_gemm_swiglu(int dtype, const void* X, const int32_t* offsets, const void* W_gate,
+                           const void* W_val, int32_t E, int64_t A, int64_t K, int64_t N,
+                           void* hidden, void* gate, void* value, void* ws, size_t ws_bytes,
+                           hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, X, W_gate, offsets, hidden);
+  if (st != NT_OK) return st;
+  if (A > 0 && N > 0 && (gate == nullptr || value == nullptr || (K > 0 && W_val == nullptr)))
+    return NT_ERR_INVALID_ARG;
+  if (A == 0 || N == 0) return NT_OK;
+  GemmArgs g{X, W_gate, offsets, E, A, K, N, hidden, 0, 0, 0, gate, nullptr, 0, nullptr,
+             nullptr, W_val, value, nullptr};
+  const uintptr_t al = reinterpret_cast<uintptr_t>(W_val) | reinterpret_cast<uintptr_t>(gate) |
+                       reinterpret_cast<uintptr_t>(value);
+  const bool mfma = mfma_ok(dtype, K, N, X, W_gate, hidden) && al % 16 == 0;
+  return launch_mode<kFwd, kEpiSwiGLU>(dtype, g, N, mfma, stream);
+}
+
+int nt_grouped_gemm_dx_swiglu(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+                              const void* gate, const void* value, int32_t E, int64_t A,
+                              int64_t K, int64_t N, void* dgate, void* dvalue, void* ws,
+                              size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate);
+  if (st != NT_OK) return st;
+  if (A > 0 && K > 0 && (dvalue == nullptr || gate == nullptr || value == nullptr))
+    return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0) return NT_OK;
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dgate, 0, 0, 0, dvalue, gate, 0, nullptr,
+             nullptr, nullptr, nullptr, value};
+  const uintptr_t al = reinterpret_cast<uintptr_t>(dvalue) | reinterpret_cast<uintptr_t>(gate) |
+                       reinterpret_cast<uintptr_t>(value);
+  const bool mfma = mfma_ok(dtype, K, N, dOut, W, dgate) && al % 16 == 0;
+  return launch_mode<kDx, kEpiSwiGLUGrad>(dtype, g, K, mfma, stream);
+}
+
+int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t* offsets,
+                        const void* dOut1, const void* dOut2, int32_t E, int64_t A, int64_t K,
+                        int64_t N, void* dX, void* ws, size_t ws_bytes, hipStream_t stream) {
+  (void)ws;
+  (void)ws_bytes;
+  int st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX);
+  if (st != NT_OK) return st;
+  if (A > 0 && N > 0 && K > 0 && (W2 == nullptr || dOut2 == nullptr)) return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0) return NT_OK;
+  GemmArgs g{dOut1, W1, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr,
+             dOut2, W2, nullptr, nullptr};
+  // The MFMA path switches operands at a k-step boundary: N a multiple of 64.
+  const uintptr_t al = reinterpret_cast<uintptr_t>(W2) | reinterpret_cast<uintptr_t>(dOut2);
+  const bool mfma = mfma_ok(dtype, K, N, dOut1, W1, dX) && al % 16 == 0 && N % 64 == 0;
+  return launch_mode<kDx, kEpiDualK>(dtype, g, K, mfma, stream);
 }
 
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,

@@ -327,6 +327,81 @@ Tensor bwd_grouped_gemm_dX_gelu(Tensor W, Tensor offsets, Tensor dOut, Tensor ac
   return dH;
 }
 
+// Checks a [rows, cols] activation that travels with W's dtype and device.
+void check_act(const Tensor& t, int64_t rows, int64_t cols, const Tensor& like, const char* name) {
+  TORCH_CHECK(t.is_contiguous() && t.dim() == 2 && t.size(0) == rows && t.size(1) == cols &&
+                  t.scalar_type() == like.scalar_type(),
+              name, ": expected a contiguous [", rows, ",", cols, "] tensor in the weights' dtype");
+  check_device(t, name);
+}
+
+// grouped_gemm_swiglu(X, expert_offset, W_gate, W_val) -> (hidden, gate, value),
+// each [A, N]: gate and value GEMMs in one kernel, hidden = silu(gate) * value
+// in its epilogue.
+std::tuple<Tensor, Tensor, Tensor> grouped_gemm_swiglu(Tensor X, Tensor offsets, Tensor Wg,
+                                                       Tensor Wv) {
+  check_gemm_inputs(X, offsets, Wg);
+  check_gemm_inputs(X, offsets, Wv);
+  TORCH_CHECK(X.dim() == 2 && Wg.dim() == 3 && Wg.size(1) == X.size(1) && Wv.sizes() == Wg.sizes(),
+              "expected X [A,K] and gate / value weights [E,K,N]");
+  TORCH_CHECK(offsets.numel() == Wg.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = X.size(0), K = X.size(1), N = Wg.size(2);
+  const int32_t E = (int32_t)Wg.size(0);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor hidden = at::empty({A, N}, X.options());
+  Tensor gate = at::empty({A, N}, X.options());
+  Tensor value = at::empty({A, N}, X.options());
+  check_status(nt_grouped_gemm_swiglu(dtype_code(X), X.data_ptr(), offsets.data_ptr<int32_t>(),
+                                      Wg.data_ptr(), Wv.data_ptr(), E, A, K, N, hidden.data_ptr(),
+                                      gate.data_ptr(), value.data_ptr(), nullptr, 0, stream_of(X)),
+               "grouped_gemm_swiglu");
+  return {hidden, gate, value};
+}
+
+// bwd_grouped_gemm_dX_swiglu(W_out, expert_offset, dOut, gate, value) ->
+// (dgate, dvalue), each [A, K]: dhidden = dOut @ W_out^T and the SwiGLU
+// backward in one kernel.
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dX_swiglu(Tensor W, Tensor offsets, Tensor dOut,
+                                                      Tensor gate, Tensor value) {
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(W.dim() == 3 && dOut.dim() == 2 && dOut.size(1) == W.size(2),
+              "expected W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = dOut.size(0), K = W.size(1), N = W.size(2);
+  check_act(gate, A, K, W, "gate");
+  check_act(value, A, K, W, "value");
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(W.get_device());
+  Tensor dgate = at::empty({A, K}, W.options());
+  Tensor dvalue = at::empty({A, K}, W.options());
+  check_status(nt_grouped_gemm_dx_swiglu(dtype_code(W), W.data_ptr(), offsets.data_ptr<int32_t>(),
+                                         dOut.data_ptr(), gate.data_ptr(), value.data_ptr(), E, A,
+                                         K, N, dgate.data_ptr(), dvalue.data_ptr(), nullptr, 0,
+                                         stream_of(W)),
+               "bwd_grouped_gemm_dX_swiglu");
+  return {dgate, dvalue};
+}
+
+// bwd_grouped_gemm_dX2(W1, W2, expert_offset, dOut1, dOut2) -> dX [A, K] =
+// dOut1 @ W1^T + dOut2 @ W2^T per expert, one reduction, one rounding.
+Tensor bwd_grouped_gemm_dX2(Tensor W1, Tensor W2, Tensor offsets, Tensor dOut1, Tensor dOut2) {
+  check_gemm_inputs(dOut1, offsets, W1);
+  check_gemm_inputs(dOut2, offsets, W2);
+  TORCH_CHECK(W1.dim() == 3 && W2.sizes() == W1.sizes() && dOut1.dim() == 2 &&
+                  dOut1.size(1) == W1.size(2) && dOut2.sizes() == dOut1.sizes(),
+              "expected W1, W2 [E,K,N] and dOut1, dOut2 [A,N]");
+  TORCH_CHECK(offsets.numel() == W1.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = dOut1.size(0), K = W1.size(1), N = W1.size(2);
+  const int32_t E = (int32_t)W1.size(0);
+  c10::hip::HIPGuard guard(W1.get_device());
+  Tensor dX = at::empty({A, K}, W1.options());
+  check_status(nt_grouped_gemm_dx2(dtype_code(W1), W1.data_ptr(), W2.data_ptr(),
+                                   offsets.data_ptr<int32_t>(), dOut1.data_ptr(), dOut2.data_ptr(),
+                                   E, A, K, N, dX.data_ptr(), nullptr, 0, stream_of(W1)),
+               "bwd_grouped_gemm_dX2");
+  return dX;
+}
+
 // ------------------------------------------------------- layer extensions
 
 // Fused router gate: (gates [T,k] f32, topk [T,k] i32).
@@ -485,6 +560,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Expert-grouped GEMM input gradient");
   m.def("grouped_gemm_gelu", &grouped_gemm_gelu,
         "Up-projection grouped GEMM with fused GELU -> (gelu(h), gelu'(h))");
+  m.def("grouped_gemm_swiglu", &grouped_gemm_swiglu,
+        "Gate and value grouped GEMMs with fused SwiGLU -> (hidden, gate, value)");
+  m.def("bwd_grouped_gemm_dX_swiglu", &bwd_grouped_gemm_dX_swiglu,
+        "dX grouped GEMM of the down projection with the SwiGLU backward -> (dgate, dvalue)");
+  m.def("bwd_grouped_gemm_dX2", &bwd_grouped_gemm_dX2,
+        "Sum of two dX grouped GEMMs over one concatenated reduction");
   m.def("bwd_grouped_gemm_dX_gelu", &bwd_grouped_gemm_dX_gelu,
         "dX grouped GEMM with fused GELU backward -> (dOut @ W^T) * act_grad");
   m.def("dispatch_tokens", &dispatch_tokens,

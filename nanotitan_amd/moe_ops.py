@@ -174,6 +174,53 @@ def grouped_gelu_ffn_fn(X, W_up, W_down, expert_offset):
     return GroupedGeluFFN_FN.apply(X, expert_offset, W_up, W_down)
 
 
+class SwiGLUFFN_FN(torch.autograd.Function):
+    """The reference's SwiGLU ExpertFFN on fused grouped GEMMs.
+
+    Forward: (h, g, v) = grouped_gemm_swiglu(X, W_gate, W_val) — the gate and
+    value GEMMs in one kernel whose epilogue writes gate, value and
+    hidden = silu(gate) * value — then y = h W_out. Backward:
+    (dgate, dvalue) from one kernel (dhidden = dy W_out^T and the SwiGLU
+    backward in its epilogue), dX = dgate W_gate^T + dvalue W_val^T as one
+    GEMM over the concatenated reduction, and the three weight gradients.
+    The values of the reference's _forward_cuda (src/model/feed_fwd.py:102-112:
+    grouped_gemm_fn, grouped_gemm_fn, silu(gate) * value, grouped_gemm_fn),
+    rounded where it rounds, except that the two dX products are summed
+    before the one rounding; backward returns
+    (dX, None, dW_gate, dW_val, dW_out).
+    """
+
+    @staticmethod
+    def forward(ctx, X, expert_offset, W_gate, W_val, W_out):
+        ext = get_hip_extension()
+        h, g, v = ext.grouped_gemm_swiglu(X, expert_offset, W_gate, W_val)
+        y = ext.grouped_gemm_kernel(h, expert_offset, W_out)
+        ctx.save_for_backward(X, expert_offset, W_gate, W_val, W_out, h, g, v)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        ext = get_hip_extension()
+        X, expert_offset, W_gate, W_val, W_out, h, g, v = ctx.saved_tensors
+        dy = dy.contiguous()
+        dX = dW_gate = dW_val = dW_out = None
+        if ctx.needs_input_grad[4]:
+            dW_out = ext.bwd_grouped_gemm_dW_kernel(h, expert_offset, dy)
+        if any(ctx.needs_input_grad[i] for i in (0, 2, 3)):
+            dg, dv = ext.bwd_grouped_gemm_dX_swiglu(W_out, expert_offset, dy, g, v)
+            if ctx.needs_input_grad[0]:
+                dX = ext.bwd_grouped_gemm_dX2(W_gate, W_val, expert_offset, dg, dv)
+            if ctx.needs_input_grad[2]:
+                dW_gate = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dg)
+            if ctx.needs_input_grad[3]:
+                dW_val = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dv)
+        return dX, None, dW_gate, dW_val, dW_out
+
+
+def swiglu_ffn_fn(X, W_gate, W_val, W_out, expert_offset):
+    return SwiGLUFFN_FN.apply(X, expert_offset, W_gate, W_val, W_out)
+
+
 # --------------------------------------------------------------- layer ops
 
 
