@@ -107,6 +107,18 @@ int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, i
                 void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
                 int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/* Tokens per block of the dispatch's counting / packing for these sizes
+ * (the TB of nt_route_topk_count); 0 for invalid sizes. */
+int32_t nt_dispatch_block_tokens(int64_t T, int32_t k, int64_t d, int dtype);
+
+/* nt_dispatch whose workspace already starts with the per-block counts of
+ * nt_route_topk_count (TB = nt_dispatch_block_tokens(T, k, d, dtype)): the
+ * same outputs, without the counting pass. */
+int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                        int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                        void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                        int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------- combine */
 
 /* Workspace for the token-id (CSR) forms of combine and pack backward. */
@@ -171,6 +183,18 @@ int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int
  * Replaces the torch glue of reference src/model/cuda_backend.py:30-37. */
 int nt_route_topk(const float* logits, int64_t T, int32_t E, int32_t k, float* gates,
                   int32_t* topk, float* probs, hipStream_t stream);
+
+/* nt_route_topk with the expert count fused in: the same gates / topk /
+ * probs, plus hist[e*nb + b] = #{(t, j) : b*TB <= t < (b+1)*TB, topk[t,j] = e}
+ * for every block b < nb = ceil(T/TB), each entry written (no zero-fill
+ * needed). With TB = nt_dispatch_block_tokens(T, k, d, dtype) and hist at
+ * the start of the dispatch workspace, nt_dispatch_counted skips its own
+ * counting pass. E <= NT_MAX_EXPERTS. Replaces the router glue and
+ * count_expert_kernel (reference src/model/cuda_backend.py:30-52,
+ * csrc/kernels/count_experts.cu:8-57). */
+int nt_route_topk_count(const float* logits, int64_t T, int32_t E, int32_t k, float* gates,
+                        int32_t* topk, float* probs, int32_t TB, int32_t* hist,
+                        hipStream_t stream);
 
 /* Gradient of nt_route_topk's gates: dlogits [T,E] f32, zero except at the
  * selected experts, where dlogits = gate * (dgate - sum_j dgate_j * gate_j). */

@@ -44,6 +44,12 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         [c_int, _P, _P, _P, c_int64, c_int32, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P,
          c_size_t, _P],
     ),
+    "nt_dispatch_counted": (
+        c_int,
+        [c_int, _P, _P, _P, c_int64, c_int32, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P,
+         c_size_t, _P],
+    ),
+    "nt_dispatch_block_tokens": (c_int32, [c_int64, c_int32, c_int64, c_int]),
     "nt_combine_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "nt_combine_tokens": (
         c_int,
@@ -71,6 +77,10 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         [c_int, _P, _P, _P, c_int64, c_int32, c_int64, _P, _P, _P],
     ),
     "nt_route_topk": (c_int, [_P, c_int64, c_int32, c_int32, _P, _P, _P, _P]),
+    "nt_route_topk_count": (
+        c_int,
+        [_P, c_int64, c_int32, c_int32, _P, _P, _P, c_int32, _P, _P],
+    ),
     "nt_route_topk_backward": (c_int, [_P, _P, _P, c_int64, c_int32, c_int32, _P, _P]),
     "nt_grouped_gemm_workspace_bytes": (c_size_t, [c_int, c_int32, c_int64, c_int64, c_int64]),
     "nt_grouped_gemm": (

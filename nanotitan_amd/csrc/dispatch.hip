@@ -348,10 +348,23 @@ int nt_pack_tokens(int dtype, const void* X, const float* w, const int32_t* topk
                             token_id, expert, packed_w, inv, stream);
 }
 
-int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
-                int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
-                void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w, int32_t* inv,
-                void* ws, size_t ws_bytes, hipStream_t stream) {
+int32_t nt_dispatch_block_tokens(int64_t T, int32_t k, int64_t d, int dtype) {
+  if (T < 0 || k < 1 || d < 0 || dtype_bytes(dtype) == 0) return 0;
+  return plan_pack(T, k, d * dtype_bytes(dtype)).TB;
+}
+
+}  // extern "C"
+
+namespace nt {
+namespace {
+
+// nt_dispatch / nt_dispatch_counted: counted = the per-block histogram is
+// already in ws (written by nt_route_topk_count); otherwise hist_kernel
+// builds it.
+int dispatch_impl(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                  int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                  void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                  int32_t* inv, void* ws, size_t ws_bytes, bool counted, hipStream_t stream) {
   int st = check_common(T, k, E);
   if (st != NT_OK) return st;
   const int eb = dtype_bytes(dtype);
@@ -363,7 +376,13 @@ int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, i
   const PackPlan plan = plan_pack(T, k, d * eb);
   if (ws == nullptr || ws_bytes < dispatch_ws_bytes(plan, E)) return NT_ERR_WORKSPACE;
   int32_t* hist = static_cast<int32_t*>(ws);
-  st = launch_hist_scan(plan, topk, nullptr, T, k, E, hist, counts, nullptr, nullptr, stream);
+  if (counted) {
+    hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, plan.nb,
+                       counts, nullptr, nullptr);
+    st = launch_status();
+  } else {
+    st = launch_hist_scan(plan, topk, nullptr, T, k, E, hist, counts, nullptr, nullptr, stream);
+  }
   if (st != NT_OK) return st;
   if (plan.nb == 0) {
     // No tokens: offsets are all zero.
@@ -373,6 +392,27 @@ int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, i
   }
   return pack_rows_dispatch(plan, X, packed_X, w, topk, T, k, E, hist, 1, nullptr, counts,
                             offsets, token_id, expert, packed_w, inv, stream);
+}
+
+}  // namespace
+}  // namespace nt
+
+extern "C" {
+
+int nt_dispatch(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w, int32_t* inv,
+                void* ws, size_t ws_bytes, hipStream_t stream) {
+  return dispatch_impl(dtype, X, w, topk, T, k, d, E, counts, offsets, packed_X, token_id,
+                       expert, packed_w, inv, ws, ws_bytes, false, stream);
+}
+
+int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                        int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                        void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                        int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream) {
+  return dispatch_impl(dtype, X, w, topk, T, k, d, E, counts, offsets, packed_X, token_id,
+                       expert, packed_w, inv, ws, ws_bytes, true, stream);
 }
 
 }  // extern "C"

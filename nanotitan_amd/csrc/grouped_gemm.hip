@@ -540,6 +540,9 @@ struct StageLoader {
   typedef OperandTile<BM, AK, BK, NW> TA;
   typedef OperandTile<DUAL == 1 ? BN / 2 : BN, BKM, BK, NW> TB;
   static constexpr int kBBytes = (DUAL == 1 ? 2 : 1) * TB::kBytes;
+  static constexpr int kBK = BK;
+  static constexpr bool kAK = AK;
+  static constexpr bool kBKM = BKM;
   static constexpr int kLoads = TA::kPer + (DUAL == 1 ? 2 : 1) * TB::kPer;  // per wave
   TA ta;
   TB tb;
@@ -1030,11 +1033,13 @@ gg_mfma_kernel(GemmArgs g) {
   constexpr int TNO = kDual == 1 ? TN / 2 : TN;
   constexpr bool kLdsEpi = TNO == 2 || TNO == 4;
   constexpr int kRows = !kLdsEpi || NW * epi_bytes<TNO, 32>() <= kStage ? 32 : 16;
-  constexpr int kStores =
+  constexpr int kStoresAll =
       !kLdsEpi ? 0
                : (kDual == 1 ? 3 * epi_stores<kEpiPlain, kRows, TM, TNO>()
                              : epi_stores<EPI, kRows, TM, TN>());
-  static_assert((NS - 2) * kLoadsPerStage + kStores < 64, "vmcnt range");
+  // Beyond the counter's range the next tile simply waits for the stores.
+  constexpr bool kDrain = (NS - 2) * kLoadsPerStage + kStoresAll < 64;
+  constexpr int kStores = kDrain ? kStoresAll : 0;
   bool stores_out = false;
   while (true) {
     zero_acc<T>(acc);
@@ -1127,16 +1132,204 @@ gg_mfma_kernel(GemmArgs g) {
           for (int v = 0; v < 16; ++v)
             part[i][jn][v] = swiglu_hidden<T>(acc[i][jn][v], acc[i][jn + TNO][v]);
       store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
-      stores_out = more;
+      stores_out = kDrain && more;
     } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
       store_tile_lds<T, EPI, kTab, kRows>(acc, job, wm * WM, wn * WN, lane,
                                           smem + (NS - 1) * kStage + wave * epi_bytes<TN, kRows>(),
                                           s_gtab);
-      stores_out = more;
+      stores_out = kDrain && more;
     } else {
       store_tile<T>(acc, job, wm * WM, wn * WN, lane);
+    }
+    if (!more) break;
+    job = nj;
+    logical = next;
+  }
+}
+
+// ------------------------------------------ 4-wave, register-staged kernel
+//
+// One workgroup of 4 waves (one per SIMD) per CU and a 256 x 256 tile:
+// each wave owns 128 x 128 outputs (TM = TN = 4, 256 accumulators, which
+// the compiler keeps in AGPRs). Operand stages are fetched with buffer loads
+// into registers two k-steps ahead of their use (two register stages,
+// 64 VGPRs each), written to an LDS slot with ds_write_b128 one k-step
+// ahead, and read from LDS like the 8-wave kernel's stages (same layouts,
+// same fragment reads). The compiler sees every load, so its own vmcnt
+// waits keep the next stage's loads and the epilogue's stores in flight.
+
+// Buffer descriptor for operand loads into registers (wave-uniform base).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = (int32_t)(bytes <= 0 ? 0 : (bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32))
+                      << 32);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0,
+                                           __builtin_amdgcn_readfirstlane(n), (int)kBufConfig);
+}
+
+// A stage in registers: the lane -> (row, chunk) map of OperandTile, so that
+// store() puts every chunk where OperandTile's LDS loads would have.
+template <typename TA, typename TB, int NW>
+struct RegStage {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 a[TA::kPer];
+  u32x4 b[TB::kPer];
+
+  template <typename L>
+  __device__ __forceinline__ void load(const L& ld, int64_t kt) {
+    constexpr int BK = L::kBK;
+    const int64_t kl = kt * BK;
+    const int64_t kleft = ld.kred - kl;
+    const int64_t kv = kleft < BK ? kleft : BK;
+    const int64_t ra = L::kAK ? ((ld.rv - 1) * ld.lda + kv) * 2 : ((kv - 1) * ld.lda + ld.rv) * 2;
+    const int64_t rb = L::kBKM ? ((ld.cv - 1) * ld.ldb + kv) * 2 : ((kv - 1) * ld.ldb + ld.cv) * 2;
+    const __amdgpu_buffer_rsrc_t rsa = in_rsrc(ld.pa + (L::kAK ? kl : kl * ld.lda), ra);
+    const __amdgpu_buffer_rsrc_t rsb = in_rsrc(ld.pb + (L::kBKM ? kl : kl * ld.ldb), rb);
+    uint32_t va = ld.ta.off, vb = ld.tb.off;
+    if (L::kAK && kv < BK && (int64_t)ld.ta.kchunk >= kv) va = kOob;
+    if (L::kBKM && kv < BK && (int64_t)ld.tb.kchunk >= kv) vb = kOob;
+#pragma unroll
+    for (int u = 0; u < TA::kPer; ++u)
+      a[u] = __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)(va + (uint32_t)u * ld.ta.ustep), 0, 0);
+#pragma unroll
+    for (int u = 0; u < TB::kPer; ++u)
+      b[u] = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(vb + (uint32_t)u * ld.tb.ustep), 0, 0);
+  }
+  __device__ __forceinline__ void store(char* lds, int wave, int lane) const {
+    char* pa = lds + wave * 1024 + lane * 16;
+    char* pb = pa + TA::kBytes;
+#pragma unroll
+    for (int u = 0; u < TA::kPer; ++u) *reinterpret_cast<u32x4*>(pa + u * NW * 1024) = a[u];
+#pragma unroll
+    for (int u = 0; u < TB::kPer; ++u) *reinterpret_cast<u32x4*>(pb + u * NW * 1024) = b[u];
+  }
+};
+
+template <typename T, int MODE, int EPI>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gg_mfma4_kernel(GemmArgs g) {
+  constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, BK = 64;
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  static_assert(EPI == kEpiPlain || EPI == kEpiGelu || EPI == kEpiGeluGrad,
+                "plain and GELU epilogues");
+  constexpr bool kAK = MODE != kDw;
+  constexpr bool kBKm = MODE == kDx;
+  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW> Loader;
+  typedef RegStage<typename Loader::TA, typename Loader::TB, NW> Stage;
+  constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
+  constexpr bool kTab = EPI == kEpiGelu && std::is_same<T, bf16>::value;
+  __shared__ uint32_t s_gtab[kTab ? kGeluTabWords : 1];
+
+  int64_t mtiles;
+  if (MODE != kDw) {
+    build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
+    mtiles = s_pref[g.E];
+  } else {
+    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, s_pref, s_pref + (NT_MAX_EXPERTS + 1));
+    mtiles = (int64_t)s_pref[g.E] * g.ntm;
+  }
+  const int64_t total = mtiles * g.ntn;
+  constexpr int kXcd = 8;
+  const int64_t G = gridDim.x;
+  const int xcd = blockIdx.x % kXcd;
+  const int64_t q = G / kXcd, r = G % kXcd;
+  const int64_t before = xcd * q + (xcd < r ? xcd : r);
+  const int64_t nbx = q + (xcd < r ? 1 : 0);
+  const int64_t t_end = total * (before + nbx) / G;
+  int64_t logical = total * before / G + blockIdx.x / kXcd;
+  if (logical >= t_end) return;
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave / WGN, wn = wave % WGN;
+  if constexpr (kTab) {
+    for (int i = threadIdx.x; i < kGeluTabWords; i += NW * kWave) s_gtab[i] = kGeluTab[i];
+  }
+  FragReader<BM, kAK, TM, BK> fa;
+  FragReader<BN, kBKm, TN, BK> fb;
+  fa.init(wm * WM, lane);
+  fb.init(wn * WN, lane);
+
+  TileJob job;
+  setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, logical, job);
+  Loader ld;
+  ld.init(job, wave, lane);
+  int64_t nk = ceil_div(job.kred, BK);
+  Stage R0, R1;
+  if (nk > 0) R0.load(ld, 0);
+  if (nk > 1) R1.load(ld, 1);
+
+  typedef typename mfma_op<T>::vec vec;
+  f32x16_t acc[TM][TN];
+  auto compute = [&](const char* sa, const char* sb) {
+    vec av[2][TM], bv[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) av[0][i] = fa.template read<vec>(sa, i, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bv[0][j] = fb.template read<vec>(sb, j, 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = fb.template read<vec>(sb, j, ks + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_op<T>::run(bv[cur][j], av[cur][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Iteration kt: Rn holds stage kt+1 (loaded two iterations ago); it goes
+  // to the LDS slot not being read (its readers passed the last barrier),
+  // then receives stage kt+3; stage kt is multiplied from slot `cur`.
+  auto step = [&](int64_t kt, Stage& Rn, int cur) {
+    if (kt + 1 < nk) Rn.store(smem + (cur ^ 1) * kStage, wave, lane);
+    if (kt + 3 < nk) Rn.load(ld, kt + 3);
+    compute(smem + cur * kStage, smem + cur * kStage + Loader::TA::kBytes);
+    __syncthreads();
+  };
+
+  while (true) {
+    zero_acc<T>(acc);
+    // Stage 0 into slot 0 (the previous tile's epilogue used slot 1),
+    // stage 2 into R0.
+    if (nk > 0) R0.store(smem, wave, lane);
+    if (nk > 2) R0.load(ld, 2);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; kt += 2) {
+      step(kt, R1, 0);
+      if (kt + 1 < nk) step(kt + 1, R0, 1);
+    }
+    // The next tile's first two stages load behind this tile's epilogue.
+    const int64_t next = logical + nbx;
+    const bool more = next < t_end;
+    TileJob nj;
+    if (more) {
+      setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, next, nj);
+      ld.init(nj, wave, lane);
+      nk = ceil_div(nj.kred, BK);
+      if (nk > 0) R0.load(ld, 0);
+      if (nk > 1) R1.load(ld, 1);
+    }
+    if (MODE == kDw && job.pf != nullptr) {
+      store_partial(acc, job, wm * WM, wn * WN, lane);
+    } else {
+      static_assert(NW * epi_bytes<TN, 32>() <= kStage, "epilogue scratch fits one slot");
+      store_tile_lds<T, EPI, kTab, 32>(acc, job, wm * WM, wn * WN, lane,
+                                       smem + kStage + wave * epi_bytes<TN, 32>(), s_gtab);
     }
     if (!more) break;
     job = nj;
@@ -1340,6 +1533,24 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
     hipLaunchKernelGGL(kb, grid, dim3(threads), 0, s, g);
   else
     hipLaunchKernelGGL(kh, grid, dim3(threads), 0, s, g);
+  return launch_status();
+}
+
+// The 4-wave register-staged kernel (256x256 tiles, one workgroup per CU).
+template <int MODE, int EPI>
+int launch_mfma4(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
+  const int64_t tiles = plan_tiles<MODE>(g, out_cols, 256, 256);
+  if (tiles == 0) return NT_OK;
+  if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
+  auto kb = gg_mfma4_kernel<bf16, MODE, EPI>;
+  auto kh = gg_mfma4_kernel<f16, MODE, EPI>;
+  static const int per_cu = blocks_per_cu(kb, 256);
+  const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
+  const dim3 grid((unsigned)nblocks);
+  if (dtype == NT_BF16)
+    hipLaunchKernelGGL(kb, grid, dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL(kh, grid, dim3(256), 0, s, g);
   return launch_status();
 }
 

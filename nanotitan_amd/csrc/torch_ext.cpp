@@ -420,6 +420,30 @@ std::tuple<Tensor, Tensor> route_topk(Tensor logits, int64_t k) {
   return {gates, topk};
 }
 
+// Router gate fused with the expert count: (gates, topk, dispatch workspace)
+// where the workspace already holds the per-block expert counts that
+// dispatch_tokens_counted(X, ...) starts from. X only fixes the dispatch's
+// block size (its row bytes) and device.
+std::tuple<Tensor, Tensor, Tensor> route_topk_count(Tensor logits, int64_t k, Tensor X) {
+  TORCH_CHECK(logits.is_contiguous() && logits.dim() == 2, "logits must be a contiguous [T,E]");
+  check_f32(logits, "logits");
+  check_device(X, "X");
+  const int64_t T = logits.size(0), E = logits.size(1);
+  TORCH_CHECK(X.dim() == 2 && X.size(0) == T, "X must be [T,d] with the logits' T");
+  TORCH_CHECK(k >= 1 && k <= E && k <= 32, "top_k must be in [1, min(E, 32)]");
+  const int dt = dtype_code(X);
+  c10::hip::HIPGuard guard(logits.get_device());
+  Tensor gates = at::empty({T, k}, logits.options());
+  Tensor topk = at::empty({T, k}, logits.options().dtype(at::kInt));
+  Tensor ws = workspace(X, nt_dispatch_workspace_bytes(T, (int32_t)k, (int32_t)E, X.size(1), dt));
+  const int32_t TB = nt_dispatch_block_tokens(T, (int32_t)k, X.size(1), dt);
+  check_status(nt_route_topk_count(logits.data_ptr<float>(), T, (int32_t)E, (int32_t)k,
+                                   gates.data_ptr<float>(), topk.data_ptr<int32_t>(), nullptr, TB,
+                                   static_cast<int32_t*>(ws.data_ptr()), stream_of(logits)),
+               "route_topk_count");
+  return {gates, topk, ws};
+}
+
 Tensor route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int64_t num_experts) {
   TORCH_CHECK(gates.is_contiguous() && topk.is_contiguous() && dgates.is_contiguous(),
               "inputs must be contiguous");
@@ -441,8 +465,8 @@ Tensor route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int64_t num
 
 // Fused count + scan + pack: (counts [E], offsets [E+1], packed_X, token_id,
 // expert, packed_w, inv [T,k]).
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens(
-    Tensor X, Tensor w, Tensor topk, int64_t num_experts) {
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_impl(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts, c10::optional<Tensor> counted_ws) {
   TORCH_CHECK(X.is_contiguous() && w.is_contiguous() && topk.is_contiguous(),
               "inputs must be contiguous");
   check_device(X, "X");
@@ -462,15 +486,36 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_toke
   Tensor expert = at::empty({A}, i32);
   Tensor packed_w = at::empty({A}, X.options().dtype(at::kFloat));
   Tensor inv = at::empty({T, k}, i32);
-  Tensor ws = workspace(X, nt_dispatch_workspace_bytes(T, (int32_t)k, E, d, dt));
-  check_status(nt_dispatch(dt, X.data_ptr(), w.data_ptr<float>(), topk.data_ptr<int32_t>(), T,
-                           (int32_t)k, d, E, counts.data_ptr<int32_t>(),
-                           offsets.data_ptr<int32_t>(), packed_X.data_ptr(),
-                           token_id.data_ptr<int32_t>(), expert.data_ptr<int32_t>(),
-                           packed_w.data_ptr<float>(), inv.data_ptr<int32_t>(), ws.data_ptr(),
-                           ws.numel(), stream_of(X)),
+  const size_t ws_need = nt_dispatch_workspace_bytes(T, (int32_t)k, E, d, dt);
+  Tensor ws;
+  if (counted_ws.has_value()) {
+    ws = *counted_ws;
+    check_device(ws, "dispatch workspace");
+    TORCH_CHECK(ws.is_contiguous() && (size_t)ws.numel() * ws.element_size() >= ws_need,
+                "dispatch workspace from route_topk_count is too small for these sizes");
+  } else {
+    ws = workspace(X, ws_need);
+  }
+  auto fn = counted_ws.has_value() ? nt_dispatch_counted : nt_dispatch;
+  check_status(fn(dt, X.data_ptr(), w.data_ptr<float>(), topk.data_ptr<int32_t>(), T, (int32_t)k,
+                  d, E, counts.data_ptr<int32_t>(), offsets.data_ptr<int32_t>(),
+                  packed_X.data_ptr(), token_id.data_ptr<int32_t>(), expert.data_ptr<int32_t>(),
+                  packed_w.data_ptr<float>(), inv.data_ptr<int32_t>(), ws.data_ptr(),
+                  (size_t)ws.numel() * ws.element_size(), stream_of(X)),
                "dispatch_tokens");
   return {counts, offsets, packed_X, token_id, expert, packed_w, inv};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts) {
+  return dispatch_impl(X, w, topk, num_experts, c10::nullopt);
+}
+
+// dispatch_tokens starting from the per-block counts route_topk_count left
+// in `ws` (no counting pass).
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens_counted(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts, Tensor ws) {
+  return dispatch_impl(X, w, topk, num_experts, ws);
 }
 
 // pack_tokens_kernel plus the inverse map.
@@ -575,6 +620,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("combine_backward_inv", &combine_backward_inv, "Combine backward driven by the inverse map");
   m.def("pack_backward_inv", &pack_backward_inv, "Pack backward driven by the inverse map");
   m.def("route_topk", &route_topk, "Fused softmax / top-k / renorm router gate -> (gates, topk)");
+  m.def("route_topk_count", &route_topk_count,
+        "Router gate fused with the per-block expert count -> (gates, topk, dispatch workspace)");
+  m.def("dispatch_tokens_counted", &dispatch_tokens_counted,
+        "dispatch_tokens from the counts route_topk_count computed");
   m.def("route_topk_backward", &route_topk_backward, "Gradient of route_topk's gates -> dlogits");
   m.def("version", []() { return nt_version(); });
 }

@@ -6,7 +6,8 @@
   offsets, pack, experts, combine, cast, and ``MoELayerStats``. It takes the
   four-argument constructor that ``MoE.__init__`` uses
   (src/model/feed_fwd.py:142; the reference class only accepts three).
-  Count + offsets + pack run as one fused native call and the combine writes
+  The router kernel emits the per-block expert counts, offsets + pack run as
+  one native call after it, and the combine writes
   the activation dtype directly (same values as combine-to-fp32-then-cast).
 * ``ExpertFFN(cfg, spec)`` — SwiGLU experts with ``[E,d,f]`` / ``[E,f,d]``
   weights (src/model/feed_fwd.py:39-122), three grouped GEMMs.
@@ -31,6 +32,7 @@ from nanotitan_amd.moe_ops import (
     combine_inv_fn,
     dispatch_fn,
     grouped_gelu_ffn_fn,
+    route_count_fn,
     route_fn,
     swiglu_ffn_fn,
 )
@@ -138,11 +140,13 @@ def moe_forward_from_logits(x_flat, logits, experts, num_experts, top_k):
 
     Returns (out [T,d], counts [E], gates [T,k]).
     """
+    # The router kernel also counts the tokens per expert and per dispatch
+    # block, so the dispatch starts at its scan.
     with record_function("moe/topK"):
-        gates, idx = route(logits, top_k)
+        gates, idx, counted = route_count_fn(logits.float().contiguous(), top_k, x_flat)
     with record_function("moe/pack_tokens"):
         packed_X, packed_w, counts, offsets, _token_id, inv = dispatch_fn(
-            x_flat, gates, idx, num_experts
+            x_flat, gates, idx, num_experts, counted
         )
     with record_function("moe/expert_compute"):
         y = experts(packed_X, offsets)

@@ -17,10 +17,12 @@ reference's ``src/model/moe_ops.py:10-125``:
 Every op runs the HIP kernels through ``get_hip_extension()``; a missing
 extension raises RuntimeError, never a silent fallback.
 
-The layer uses two additional Functions built on the inverse map the pack
-writes: ``DispatchFN`` (fused count + offsets + pack) and ``CombineInvFN``
-(combine whose backward reads each token's grad row once). They compute the
-same values as pack_tokens_fn / combine_tokens_fn on the same inputs.
+The layer uses additional Functions built on the inverse map the pack
+writes: ``RouteCountFN`` (router gate that also counts the tokens per expert
+and dispatch block), ``DispatchFN`` (count + offsets + pack, or offsets + pack
+from RouteCountFN's counts) and ``CombineInvFN`` (combine whose backward reads
+each token's grad row once). They compute the same values as pack_tokens_fn /
+combine_tokens_fn on the same inputs.
 """
 
 from __future__ import annotations
@@ -233,11 +235,17 @@ class DispatchFN(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, X, topk_weights, topk_experts, num_experts):
+    def forward(ctx, X, topk_weights, topk_experts, num_experts, counted_ws=None):
+        # counted_ws: the workspace route_count_fn returned for these tokens,
+        # already holding the per-block expert counts (the counting pass is
+        # then skipped).
         ext = get_hip_extension()
-        counts, offsets, packed_X, token_id, _expert, packed_w, inv = ext.dispatch_tokens(
-            X, topk_weights, topk_experts, num_experts
-        )
+        if counted_ws is None:
+            outs = ext.dispatch_tokens(X, topk_weights, topk_experts, num_experts)
+        else:
+            outs = ext.dispatch_tokens_counted(X, topk_weights, topk_experts, num_experts,
+                                               counted_ws)
+        counts, offsets, packed_X, token_id, _expert, packed_w, inv = outs
         ctx.save_for_backward(inv)
         ctx.mark_non_differentiable(counts, offsets, token_id, inv)
         # No zero-filled grads for the integer outputs (or an unused packed_w).
@@ -255,7 +263,7 @@ class DispatchFN(torch.autograd.Function):
         X_grad, w_grad = ext.pack_backward_inv(
             packed_X_grad.contiguous(), packed_w_grad.contiguous(), inv
         )
-        return X_grad, w_grad, None, None
+        return X_grad, w_grad, None, None, None
 
 
 class CombineInvFN(torch.autograd.Function):
@@ -310,12 +318,45 @@ class RouteFN(torch.autograd.Function):
                                        ctx.num_experts), None
 
 
+class RouteCountFN(torch.autograd.Function):
+    """RouteFN with the dispatch's expert count fused into the router kernel.
+
+    Returns (gates, topk, dispatch_ws): dispatch_ws holds the per-block
+    expert counts for the tokens X (X fixes the block size and device) and
+    goes to dispatch_fn(..., counted_ws=dispatch_ws). Same gates, ids and
+    backward as RouteFN.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, top_k, X):
+        ext = get_hip_extension()
+        gates, topk, ws = ext.route_topk_count(logits.contiguous(), top_k, X)
+        ctx.save_for_backward(gates, topk)
+        ctx.num_experts = logits.shape[1]
+        ctx.mark_non_differentiable(topk, ws)
+        ctx.set_materialize_grads(False)
+        return gates, topk, ws
+
+    @staticmethod
+    def backward(ctx, dgates, _dtopk, _dws):
+        ext = get_hip_extension()
+        gates, topk = ctx.saved_tensors
+        if dgates is None:
+            return None, None, None
+        return ext.route_topk_backward(gates, topk, dgates.contiguous().float(),
+                                       ctx.num_experts), None, None
+
+
 def route_fn(logits, top_k):
     return RouteFN.apply(logits, top_k)
 
 
-def dispatch_fn(X, topk_weights, topk_experts, num_experts):
-    return DispatchFN.apply(X, topk_weights, topk_experts, num_experts)
+def route_count_fn(logits, top_k, X):
+    return RouteCountFN.apply(logits, top_k, X)
+
+
+def dispatch_fn(X, topk_weights, topk_experts, num_experts, counted_ws=None):
+    return DispatchFN.apply(X, topk_weights, topk_experts, num_experts, counted_ws)
 
 
 def combine_inv_fn(packed_expert_outputs, inv, packed_topk_weights, out_dtype=torch.float32):

@@ -41,6 +41,18 @@ def test_strerror_and_version():
     assert lib.nt_version() >= 100
 
 
+def test_dispatch_block_tokens():
+    """The router's count blocks follow the pack's: fewer tokens per block for wider rows."""
+    lib = capi.load()
+    bt = lib.nt_dispatch_block_tokens
+    assert bt(30720, 2, 4096, capi.NT_BF16) == 16
+    assert bt(30720, 2, 512, capi.NT_BF16) == 64
+    assert bt(30720, 2, 1024, capi.NT_F32) < bt(30720, 2, 1024, capi.NT_BF16)
+    assert bt(100, 32, 8, capi.NT_F32) * 32 <= 2048
+    assert bt(100, 0, 8, capi.NT_F32) == 0
+    assert bt(100, 2, 8, 99) == 0
+
+
 def test_workspace_sizes_are_sane():
     lib = capi.load()
     assert lib.nt_dispatch_workspace_bytes(30720, 2, 8, 512, capi.NT_BF16) > 0
@@ -68,6 +80,15 @@ def test_workspace_sizes_are_sane():
          capi.NT_ERR_INVALID_ARG),
         ("nt_pack_backward_inv", (capi.NT_BF16, None, None, None, -3, 2, 8, None, None, None),
          capi.NT_ERR_INVALID_ARG),
+        ("nt_route_topk_count", (None, 8, 4, 2, None, None, None, 0, None, None),
+         capi.NT_ERR_INVALID_ARG),
+        ("nt_route_topk_count", (None, 8, 4, 5, None, None, None, 16, None, None),
+         capi.NT_ERR_INVALID_ARG),
+        ("nt_route_topk_count", (None, 8, 1025, 2, None, None, None, 16, None, None),
+         capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_dispatch_counted", (capi.NT_BF16, None, None, None, 8, 2, 16, 1025, None, None,
+                                 None, None, None, None, None, None, 0, None),
+         capi.NT_ERR_TOO_MANY_EXPERTS),
     ],
 )
 def test_argument_errors_return_codes(fn, args, code):

@@ -68,6 +68,43 @@ def test_capi_dispatch_combine_roundtrip(lib, dtype):
     assert torch.equal(bits(out2), bits(out))
 
 
+def test_capi_route_count_then_dispatch_counted(lib):
+    """nt_route_topk_count writes the per-block counts at the start of the
+    dispatch workspace; nt_dispatch_counted then matches the oracle."""
+    d = O.make_inputs(2, T=3000, with_weights=False)
+    c = d["cfg"]
+    X = d["X"][:, :512].contiguous()
+    T, dd, k, E = X.shape[0], X.shape[1], c.k, c.E
+    A = T * k
+    want_g, want_i, _ = O.route(d["logits"], k)
+    counts, offsets, p = O.dispatch(X, want_g, want_i, E)
+    code = dtype_code(X.dtype)
+    TB = lib.nt_dispatch_block_tokens(T, k, dd, code)
+    nbytes = lib.nt_dispatch_workspace_bytes(T, k, E, dd, code)
+    w = ws(nbytes)
+    lg, Xg = d["logits"].cuda(), X.cuda()
+    gates = torch.empty(T, k, device="cuda")
+    topk = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    s = current_stream()
+    call("nt_route_topk_count", ptr(lg), T, E, k, ptr(gates), ptr(topk), None, TB, ptr(w), s)
+    g_counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    g_off = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    g_px = torch.empty(A, dd, dtype=X.dtype, device="cuda")
+    g_tid = torch.empty(A, dtype=torch.int32, device="cuda")
+    g_ex = torch.empty(A, dtype=torch.int32, device="cuda")
+    g_pw = torch.empty(A, dtype=torch.float32, device="cuda")
+    g_inv = torch.empty(T, k, dtype=torch.int32, device="cuda")
+    call("nt_dispatch_counted", code, ptr(Xg), ptr(gates), ptr(topk), T, k, dd, E, ptr(g_counts),
+         ptr(g_off), ptr(g_px), ptr(g_tid), ptr(g_ex), ptr(g_pw), ptr(g_inv), ptr(w), nbytes, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(topk.cpu().numpy(), want_i.numpy())
+    assert np.array_equal(g_counts.cpu().numpy(), counts)
+    assert np.array_equal(g_off.cpu().numpy(), offsets)
+    assert np.array_equal(g_tid.cpu().numpy(), p.token_id)
+    assert np.array_equal(g_inv.cpu().numpy(), p.inv)
+    assert torch.equal(bits(g_px), bits(p.packed_X))
+
+
 def test_capi_workspace_too_small(lib):
     T, k, E, dd = 64, 2, 8, 16
     z = torch.zeros(1, device="cuda")

@@ -151,3 +151,89 @@ def test_errors_raise_runtime_error(ext):
         ext.pack_tokens_kernel(X, w, topk.long(), torch.zeros(3, dtype=torch.int32, device="cuda"))
     with pytest.raises(RuntimeError):
         ext.count_expert_kernel(topk, torch.ones(4, dtype=torch.int32, device="cuda"), 2000, 2)
+
+
+def block_hist(idx: np.ndarray, E: int, TB: int) -> np.ndarray:
+    """[E, nb] expert counts of each TB-token block, by numpy bincount (independent of the kernels)."""
+    T = idx.shape[0]
+    nb = -(-T // TB)
+    out = np.zeros((E, nb), dtype=np.int32)
+    for b in range(nb):
+        out[:, b] = np.bincount(idx[b * TB:(b + 1) * TB].reshape(-1), minlength=E)
+    return out
+
+
+def check_route_count(ext, logits, k, X, E):
+    """route_topk_count + dispatch_tokens_counted vs route_topk + the oracle's dispatch."""
+    from nanotitan_amd import capi
+
+    T = logits.shape[0]
+    want_g, want_i, _ = O.route(logits, k)
+    g, i, ws = ext.route_topk_count(logits.cuda(), k, X.cuda())
+    g_ref, i_ref = ext.route_topk(logits.cuda(), k)
+    torch.cuda.synchronize()
+    assert np.array_equal(i.cpu().numpy(), want_i.numpy())
+    assert torch.equal(bits(g), bits(g_ref)) and torch.equal(i.cpu(), i_ref.cpu())
+    TB = capi.load().nt_dispatch_block_tokens(T, k, X.shape[1], capi.dtype_code(X.dtype))
+    nb = -(-T // TB)
+    hist = ws[: E * nb * 4].view(torch.int32).cpu().numpy().reshape(E, nb)
+    assert np.array_equal(hist, block_hist(want_i.numpy(), E, TB))
+    counts, offsets, p = O.dispatch(X, want_g, want_i, E)
+    outs = ext.dispatch_tokens_counted(X.cuda(), g, i, E, ws)
+    g_counts, g_off, g_px, g_tid, g_ex, g_pw, g_inv = outs
+    torch.cuda.synchronize()
+    assert np.array_equal(g_counts.cpu().numpy(), counts)
+    assert np.array_equal(g_off.cpu().numpy(), offsets)
+    assert np.array_equal(g_tid.cpu().numpy(), p.token_id)
+    assert np.array_equal(g_ex.cpu().numpy(), p.expert)
+    assert np.array_equal(g_inv.cpu().numpy(), p.inv)
+    assert torch.equal(bits(g_px), bits(p.packed_X))
+    # same bits as the unfused dispatch on the kernel's own gates
+    plain = ext.dispatch_tokens(X.cuda(), g, i, E)
+    for a, b in zip(outs, plain):
+        assert torch.equal(bits(a), bits(b))
+
+
+@pytest.mark.parametrize("cfg_id,T", [(1, 4096), (2, 30720), (3, 30720), (5, 65536), (5, 777)])
+def test_route_count_dispatch_config_routing(ext, cfg_id, T):
+    """Router gate fused with the count, at the configs' logits: the per-block
+    counts equal numpy's bincount and the dispatch from them equals the oracle."""
+    d = O.make_inputs(cfg_id, T=T, with_weights=False)
+    c = d["cfg"]
+    X = d["X"]
+    if cfg_id == 5:
+        X = X[:, :256].contiguous()
+    check_route_count(ext, d["logits"], c.k, X, c.E)
+
+
+@pytest.mark.parametrize("T,E,k,d,dtype", [(1, 1, 1, 8, torch.float32), (7, 3, 3, 5, torch.float16),
+                                           (1000, 16, 4, 1024, torch.float32),
+                                           (513, 1024, 32, 16, torch.bfloat16),
+                                           (2049, 128, 8, 4096, torch.bfloat16),
+                                           (300, 9, 1, 2048, torch.bfloat16)])
+def test_route_count_random(ext, T, E, k, d, dtype):
+    """Ragged block tails, E from 1 to 1024, k up to 32, every row-size plan."""
+    g_ = torch.Generator().manual_seed(T * 3 + E)
+    logits = torch.randn(T, E, generator=g_)
+    logits[::5] = torch.round(logits[::5])  # exact ties
+    X = torch.randn(T, d, generator=g_).to(dtype)
+    check_route_count(ext, logits, k, X, E)
+
+
+def test_route_count_empty(ext):
+    logits = torch.empty(0, 8, device="cuda")
+    X = torch.empty(0, 16, device="cuda", dtype=torch.bfloat16)
+    g, i, ws = ext.route_topk_count(logits, 2, X)
+    assert g.shape == (0, 2) and i.shape == (0, 2)
+    counts, offsets, px, *_ = ext.dispatch_tokens_counted(X, g, i, 8, ws)
+    assert counts.tolist() == [0] * 8 and offsets.tolist() == [0] * 9 and px.shape == (0, 16)
+
+
+def test_route_count_rejects_small_workspace(ext):
+    logits = torch.randn(64, 8, device="cuda")
+    X = torch.randn(64, 16, device="cuda")
+    g, i, ws = ext.route_topk_count(logits, 2, X)
+    with pytest.raises(RuntimeError):
+        ext.dispatch_tokens_counted(X, g, i, 8, ws[:4])
+    with pytest.raises(RuntimeError):
+        ext.route_topk_count(logits, 2, X[:10])
