@@ -199,6 +199,7 @@ constexpr int kMfmaWaves = kMfmaThreads / kWave;
 // barrier before a stage is read.
 constexpr uint32_t kBufConfig = 0x00020000u;  // gfx9 buffer descriptor word 3
 constexpr uint32_t kOob = 0x80000000u;
+constexpr int kCpolNT = 2;  // buffer instruction cache policy: non-temporal
 
 __device__ __forceinline__ i32x4_t make_rsrc(const void* base, int64_t bytes) {
   const int32_t n = (int32_t)(bytes <= 0 ? 0 : (bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
@@ -225,6 +226,13 @@ __device__ __forceinline__ void load16_to_lds(i32x4_t rsrc, uint32_t voff, uint3
       : "memory", "m0");
 }
 
+// a + b (b wave-uniform) as an instruction the compiler cannot move or fold.
+__device__ __forceinline__ uint32_t add_opaque(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm volatile("v_add_u32 %0, %1, %2" : "=v"(r) : "s"(b), "v"(a));
+  return r;
+}
+
 // Wait until at most N of this wave's vector-memory operations are in
 // flight. The counter retires loads and stores in issue order, so every
 // older operation is complete.
@@ -247,10 +255,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const void* base) {
                                            (int)kBufConfig);
 }
 
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
 __device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
   typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   const u32x4_t d = {v.x, v.y, v.z, v.w};
-  __builtin_amdgcn_raw_buffer_store_b128(d, r, (int)off, 0, 0);
+  // Non-temporal (cache policy NT): output tiles are written once and read
+  // by a later kernel, so they should not displace the operand panels the
+  // XCD's L2 shares between concurrent tiles (measured: -5 to -19 us per
+  // C2-sized GEMM).
+  __builtin_amdgcn_raw_buffer_store_b128(d, r, (int)off, 0, kCpolNT);
 }
 
 // One operand tile in LDS, ROWS (m or n) x BK (reduction, 64 or 32) 16-bit
@@ -296,7 +314,7 @@ struct OperandTile {
     const int c = KMAJ ? (lane % kCpr) ^ ((r / kRpw) % kCpr) : (lane % kCpr) ^ (4 * (r & 3));
     off = (uint32_t)((int64_t)r * ld + c * 8) * 2u;
     kchunk = (uint32_t)(c * 8);
-    ustep = (uint32_t)(NW * kRowsPerInst * ld * 2);
+    ustep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(NW * kRowsPerInst * ld * 2));
   }
 
   // Issue this wave's share of the tile's loads. `base` is the tile origin
@@ -308,10 +326,14 @@ struct OperandTile {
     const uint32_t l0 = lds_addr(lds) + (uint32_t)wave * 1024u;
     uint32_t v = off;
     if (KMAJ && kv < BK && (int64_t)kchunk >= kv) v = kOob;
+    // Instruction u reads u * ustep bytes further on. The offset advances
+    // through an opaque add, so the compiler keeps one offset register
+    // instead of hoisting kPer of them out of the k-loop.
 #pragma unroll
-    for (int u = 0; u < kPer; ++u)
-      load16_to_lds(rs, v + (uint32_t)u * ustep,
-                    __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
+    for (int u = 0; u < kPer; ++u) {
+      load16_to_lds(rs, v, __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
+      if (u + 1 < kPer) v = add_opaque(v, ustep);
+    }
   }
 };
 
@@ -816,17 +838,21 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
   // kEpiSwiGLUGrad loads two inputs (gate and value) the same way.
   constexpr bool kAux = EPI == kEpiGeluGrad || EPI == kEpiSwiGLUGrad;
   constexpr bool kAux2 = EPI == kEpiSwiGLUGrad;
+  // In-tile bounds and offsets fit 32 bits (m < 256, ldo < 2^22); 64-bit
+  // row indices would be hoisted out of the tile loop and spilled.
+  const int rv = (int)(j.rows_valid < 256 ? j.rows_valid : 256);
+  const int cv = (int)(j.cols_valid < 256 ? j.cols_valid : 256);
+  const uint32_t ldo = (uint32_t)j.ldo;
   uint4 aux[kReads], aux2[kReads];
+  // Inputs through buffer descriptors: lanes outside the tile read zeros.
+  const __amdgpu_buffer_rsrc_t ra = out_rsrc(kAux ? j.paux : j.po);
+  const __amdgpu_buffer_rsrc_t ra2 = out_rsrc(kAux2 ? j.paux2 : j.po);
   auto load_aux = [&](int i, int ps, int q) {
     const int m = m0 + i * 32 + ps * ROWS + q * kRowsPerRead + lane / kLanesPerRow;
     const int n = n0 + (lane % kLanesPerRow) * 8;
-    uint4 g = make_uint4(0u, 0u, 0u, 0u), g2 = g;
-    if (m < j.rows_valid && n < j.cols_valid) {
-      g = *reinterpret_cast<const uint4*>(j.paux + (int64_t)m * j.ldo + n);
-      if (kAux2) g2 = *reinterpret_cast<const uint4*>(j.paux2 + (int64_t)m * j.ldo + n);
-    }
-    aux[ps * (ROWS / kRowsPerRead) + q] = g;
-    aux2[ps * (ROWS / kRowsPerRead) + q] = g2;
+    const uint32_t off = (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
+    aux[ps * (ROWS / kRowsPerRead) + q] = load16(ra, off);
+    aux2[ps * (ROWS / kRowsPerRead) + q] = kAux2 ? load16(ra2, off) : make_uint4(0u, 0u, 0u, 0u);
   };
   if constexpr (kAux) {
 #pragma unroll
@@ -862,15 +888,122 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
         const uint4 v = *reinterpret_cast<const uint4*>(scratch + rr * kPitch + ch * 16);
         const int m = m0 + i * 32 + ps * ROWS + rr;
         const int n = n0 + ch * 8;
-        const uint32_t off = (m < j.rows_valid && n < j.cols_valid)
-                                 ? (uint32_t)(((int64_t)m * j.ldo + n) * 2)
-                                 : kOob;
+        const uint32_t off =
+            (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
         epilogue8<T, EPI, TAB>(v, ro, ro2, off, aux[ps * (ROWS / kRowsPerRead) + q],
                                aux2[ps * (ROWS / kRowsPerRead) + q], tab);
         if constexpr (kAux) {
           if (i + 1 < TM) load_aux(i + 1, ps, q);
         }
       }
+    }
+  }
+}
+
+// Epilogue of the 8-wave kernel with split duties: waves NW/2..NW-1 issue
+// every global store of the tile and never wait for them, so the stores
+// drain behind the next tile's k-loop (vmcnt is per wave and retires in
+// issue order: a wave that also issued the operand loads would wait for its
+// stores at its next load wait). Each round every wave rounds a 16-row half
+// of one of its 32-row sub-tiles into its LDS scratch region (applying GELU
+// there for kEpiGelu, so that VALU work stays spread over all waves; the
+// launcher uses the split for plain epilogues only); after
+// a barrier storer wave w reads back its own region and that of wave
+// w - NW/2 (16 bytes per lane, whole 128-byte row segments) and stores both;
+// a second barrier frees the scratch for the next round. `scratch` holds
+// NW * kOuts * 16 * epi_pitch<TN>() bytes.
+template <int EPI, int TN>
+constexpr int split_scratch_bytes(int nw) {
+  return nw * (EPI == kEpiGelu ? 2 : 1) * 16 * epi_pitch<TN>();
+}
+template <typename T, int EPI, bool TAB, int TM, int TN, int WGN, int WM, int WN, int NW>
+__device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+                                                 int wave, int lane, char* scratch,
+                                                 const uint32_t* tab) {
+  static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
+  static_assert(EPI == kEpiPlain || EPI == kEpiDualK || EPI == kEpiGelu,
+                "stores without epilogue inputs");
+  constexpr int ROWS = 16;
+  constexpr int kOuts = EPI == kEpiGelu ? 2 : 1;
+  constexpr int kPitch = epi_pitch<TN>();
+  constexpr int kRegion = ROWS * kPitch;  // one wave, one output
+  constexpr int kLanesPerRow = TN * 4;
+  constexpr int kRowsPerRead = 64 / kLanesPerRow;
+  constexpr int kQ = ROWS / kRowsPerRead;
+  constexpr int NL = NW / 2;
+  const bool storer = wave >= NL;
+  // In-tile bounds and offsets fit 32 bits (m < BM, ldo < 2^22).
+  const int rv = (int)(j.rows_valid < 256 ? j.rows_valid : 256);
+  const int cv = (int)(j.cols_valid < 256 ? j.cols_valid : 256);
+  const uint32_t ldo = (uint32_t)j.ldo;
+  char* mine = scratch + wave * kOuts * kRegion;
+  const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
+  const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(kOuts == 2 ? j.po2 : j.po);
+  const int r = lane & 31;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int ps = 0; ps < 32 / ROWS; ++ps) {
+      if (r / ROWS == ps) {
+        char* row = mine + (r % ROWS) * kPitch;
+#pragma unroll
+        for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+          for (int gp = 0; gp < 2; ++gp) {
+            // two 4-column groups (gq = 2gp, 2gp+1) of sub-tile (i, jn)
+            uint32_t w[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int gq = 2 * gp + h;
+              w[2 * h] = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
+              w[2 * h + 1] = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
+            }
+            uint32_t o[4], o2[4];
+            if constexpr (EPI == kEpiGelu) {
+              if constexpr (TAB) {
+                gelu8_table(w, tab, o, o2);
+              } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) gelu2_formula<T>(w[q], o[q], o2[q]);
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) o[q] = w[q];
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int c = jn * 32 + 8 * (2 * gp + h) + 4 * (lane >> 5);
+              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(o[2 * h], o[2 * h + 1]);
+              if constexpr (kOuts == 2)
+                *reinterpret_cast<uint2*>(row + kRegion + c * 2) =
+                    make_uint2(o2[2 * h], o2[2 * h + 1]);
+            }
+          }
+      }
+      __syncthreads();
+      if (storer) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int src = h == 0 ? wave - NL : wave;
+          const int sm0 = (src / WGN) * WM + i * 32 + ps * ROWS;
+          const int sn0 = (src % WGN) * WN;
+          const char* sp = scratch + src * kOuts * kRegion;
+#pragma unroll
+          for (int q = 0; q < kQ; ++q) {
+            const int rr = q * kRowsPerRead + lane / kLanesPerRow;
+            const int ch = lane % kLanesPerRow;
+            const int m = sm0 + rr;
+            const int n = sn0 + ch * 8;
+            const uint32_t off =
+                (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
+            store16(ro, off, *reinterpret_cast<const uint4*>(sp + rr * kPitch + ch * 16));
+            if constexpr (kOuts == 2)
+              store16(ro2, off,
+                      *reinterpret_cast<const uint4*>(sp + kRegion + rr * kPitch + ch * 16));
+          }
+        }
+      }
+      __syncthreads();
     }
   }
 }
@@ -921,7 +1054,8 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[TM][TN]) {
 // Tiles are dealt to XCDs in contiguous ranges (workgroup b runs on XCD
 // b % 8), so tiles that share operand panels share that XCD's L2; inside a
 // range, tile_coords walks groups of kGroupM m-tiles with m fastest.
-template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI>
+template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
+          bool SPLIT>
 __global__ void __launch_bounds__(WGM * WGN * kWave)
 gg_mfma_kernel(GemmArgs g) {
   constexpr int NW = WGM * WGN;
@@ -934,9 +1068,17 @@ gg_mfma_kernel(GemmArgs g) {
   constexpr int kDual = EPI == kEpiSwiGLU ? 1 : (EPI == kEpiDualK ? 2 : 0);
   static_assert(kDual != 1 || (MODE == kFwd && TN % 2 == 0), "SwiGLU: forward, gate|value halves");
   static_assert(kDual != 2 || MODE == kDx, "two-part reduction: dX only");
-  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW, kDual> Loader;
+  // Split duties (SPLIT; 8 waves, plain epilogues): waves 0..NW/2-1 issue
+  // every operand load, the others every output store (store_tile_split).
+  constexpr bool kSplit = SPLIT;
+  static_assert(!SPLIT || (NW == 8 && MODE != kDw && kDual != 1 &&
+                           (EPI == kEpiPlain || EPI == kEpiDualK) &&
+                           (WN / 32 == 2 || WN / 32 == 4)),
+                "split duties: 8-wave plain epilogues");
+  constexpr int NL = kSplit ? NW / 2 : NW;  // waves that issue operand loads
+  typedef StageLoader<BM, BN, kAK, kBKm, BK, NL, kDual> Loader;
   constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
-  constexpr int kLoadsPerStage = Loader::kLoads;  // per wave
+  constexpr int kLoadsPerStage = Loader::kLoads;  // per loading wave
   __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
   // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
   __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
@@ -983,14 +1125,17 @@ gg_mfma_kernel(GemmArgs g) {
   fa.init(wm * WM, lane);
   fb.init(wn * (WN * kBRows / BN), lane);
 
+  const bool loader = !kSplit || wave < NL;
   TileJob job;
   setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, logical, job);
   Loader ld;
   ld.init(job, wave, lane);
   int64_t nk = ceil_div(job.kred, BK);
+  if (loader) {
 #pragma unroll
-  for (int s0 = 0; s0 < NS - 1; ++s0)
-    if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
+    for (int s0 = 0; s0 < NS - 1; ++s0)
+      if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
+  }
 
   typedef typename mfma_op<T>::vec vec;
   f32x16_t acc[TM][TN];
@@ -1051,7 +1196,9 @@ gg_mfma_kernel(GemmArgs g) {
     int slot = 0;
     for (int64_t kt = 0; kt < nk; ++kt) {
       const int64_t younger = nk - 1 - kt;  // stages issued after this one (capped below)
-      if (kt == 0 && stores_out) {
+      if (!loader) {
+        // storer waves have no loads to wait for (only their stores)
+      } else if (kt == 0 && stores_out) {
         if (younger >= NS - 2) {
           wait_vmcnt<(NS - 2) * kLoadsPerStage + kStores>();
         } else if (NS > 3 && younger == 2) {
@@ -1071,7 +1218,7 @@ gg_mfma_kernel(GemmArgs g) {
         wait_vmcnt<0>();
       }
       __syncthreads();
-      if (kt + NS - 1 < nk) {
+      if (loader && kt + NS - 1 < nk) {
         int fill = slot + NS - 1;
         if (fill >= NS) fill -= NS;
         ld.issue(kt + NS - 1, smem + fill * kStage);
@@ -1090,9 +1237,11 @@ gg_mfma_kernel(GemmArgs g) {
       setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, next, nj);
       ld.init(nj, wave, lane);
       nk = ceil_div(nj.kred, BK);
+      if (loader) {
 #pragma unroll
-      for (int s0 = 0; s0 < NS - 1; ++s0)
-        if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
+        for (int s0 = 0; s0 < NS - 1; ++s0)
+          if (s0 < nk) ld.issue(s0, smem + s0 * kStage);
+      }
     }
     static_assert(kLdsEpi || EPI == kEpiPlain, "fused epilogues use the LDS-staged store");
     stores_out = false;
@@ -1133,6 +1282,10 @@ gg_mfma_kernel(GemmArgs g) {
             part[i][jn][v] = swiglu_hidden<T>(acc[i][jn][v], acc[i][jn + TNO][v]);
       store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
       stores_out = kDrain && more;
+    } else if constexpr (kSplit) {
+      static_assert(split_scratch_bytes<EPI, TN>(NW) <= kStage, "split scratch fits one stage");
+      store_tile_split<T, EPI, kTab, TM, TN, WGN, WM, WN, NW>(acc, job, wave, lane,
+                                                             smem + (NS - 1) * kStage, s_gtab);
     } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
@@ -1142,194 +1295,6 @@ gg_mfma_kernel(GemmArgs g) {
       stores_out = kDrain && more;
     } else {
       store_tile<T>(acc, job, wm * WM, wn * WN, lane);
-    }
-    if (!more) break;
-    job = nj;
-    logical = next;
-  }
-}
-
-// ------------------------------------------ 4-wave, register-staged kernel
-//
-// One workgroup of 4 waves (one per SIMD) per CU and a 256 x 256 tile:
-// each wave owns 128 x 128 outputs (TM = TN = 4, 256 accumulators, which
-// the compiler keeps in AGPRs). Operand stages are fetched with buffer loads
-// into registers two k-steps ahead of their use (two register stages,
-// 64 VGPRs each), written to an LDS slot with ds_write_b128 one k-step
-// ahead, and read from LDS like the 8-wave kernel's stages (same layouts,
-// same fragment reads). The compiler sees every load, so its own vmcnt
-// waits keep the next stage's loads and the epilogue's stores in flight.
-
-// Buffer descriptor for operand loads into registers (wave-uniform base).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const void* base, int64_t bytes) {
-  const int32_t n = (int32_t)(bytes <= 0 ? 0 : (bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
-                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32))
-                      << 32);
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0,
-                                           __builtin_amdgcn_readfirstlane(n), (int)kBufConfig);
-}
-
-// A stage in registers: the lane -> (row, chunk) map of OperandTile, so that
-// store() puts every chunk where OperandTile's LDS loads would have.
-template <typename TA, typename TB, int NW>
-struct RegStage {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 a[TA::kPer];
-  u32x4 b[TB::kPer];
-
-  template <typename L>
-  __device__ __forceinline__ void load(const L& ld, int64_t kt) {
-    constexpr int BK = L::kBK;
-    const int64_t kl = kt * BK;
-    const int64_t kleft = ld.kred - kl;
-    const int64_t kv = kleft < BK ? kleft : BK;
-    const int64_t ra = L::kAK ? ((ld.rv - 1) * ld.lda + kv) * 2 : ((kv - 1) * ld.lda + ld.rv) * 2;
-    const int64_t rb = L::kBKM ? ((ld.cv - 1) * ld.ldb + kv) * 2 : ((kv - 1) * ld.ldb + ld.cv) * 2;
-    const __amdgpu_buffer_rsrc_t rsa = in_rsrc(ld.pa + (L::kAK ? kl : kl * ld.lda), ra);
-    const __amdgpu_buffer_rsrc_t rsb = in_rsrc(ld.pb + (L::kBKM ? kl : kl * ld.ldb), rb);
-    uint32_t va = ld.ta.off, vb = ld.tb.off;
-    if (L::kAK && kv < BK && (int64_t)ld.ta.kchunk >= kv) va = kOob;
-    if (L::kBKM && kv < BK && (int64_t)ld.tb.kchunk >= kv) vb = kOob;
-#pragma unroll
-    for (int u = 0; u < TA::kPer; ++u)
-      a[u] = __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)(va + (uint32_t)u * ld.ta.ustep), 0, 0);
-#pragma unroll
-    for (int u = 0; u < TB::kPer; ++u)
-      b[u] = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)(vb + (uint32_t)u * ld.tb.ustep), 0, 0);
-  }
-  __device__ __forceinline__ void store(char* lds, int wave, int lane) const {
-    char* pa = lds + wave * 1024 + lane * 16;
-    char* pb = pa + TA::kBytes;
-#pragma unroll
-    for (int u = 0; u < TA::kPer; ++u) *reinterpret_cast<u32x4*>(pa + u * NW * 1024) = a[u];
-#pragma unroll
-    for (int u = 0; u < TB::kPer; ++u) *reinterpret_cast<u32x4*>(pb + u * NW * 1024) = b[u];
-  }
-};
-
-template <typename T, int MODE, int EPI>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gg_mfma4_kernel(GemmArgs g) {
-  constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, BK = 64;
-  constexpr int NW = WGM * WGN;
-  constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  static_assert(EPI == kEpiPlain || EPI == kEpiGelu || EPI == kEpiGeluGrad,
-                "plain and GELU epilogues");
-  constexpr bool kAK = MODE != kDw;
-  constexpr bool kBKm = MODE == kDx;
-  typedef StageLoader<BM, BN, kAK, kBKm, BK, NW> Loader;
-  typedef RegStage<typename Loader::TA, typename Loader::TB, NW> Stage;
-  constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
-  __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
-  constexpr bool kTab = EPI == kEpiGelu && std::is_same<T, bf16>::value;
-  __shared__ uint32_t s_gtab[kTab ? kGeluTabWords : 1];
-
-  int64_t mtiles;
-  if (MODE != kDw) {
-    build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
-    mtiles = s_pref[g.E];
-  } else {
-    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, s_pref, s_pref + (NT_MAX_EXPERTS + 1));
-    mtiles = (int64_t)s_pref[g.E] * g.ntm;
-  }
-  const int64_t total = mtiles * g.ntn;
-  constexpr int kXcd = 8;
-  const int64_t G = gridDim.x;
-  const int xcd = blockIdx.x % kXcd;
-  const int64_t q = G / kXcd, r = G % kXcd;
-  const int64_t before = xcd * q + (xcd < r ? xcd : r);
-  const int64_t nbx = q + (xcd < r ? 1 : 0);
-  const int64_t t_end = total * (before + nbx) / G;
-  int64_t logical = total * before / G + blockIdx.x / kXcd;
-  if (logical >= t_end) return;
-
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int wm = wave / WGN, wn = wave % WGN;
-  if constexpr (kTab) {
-    for (int i = threadIdx.x; i < kGeluTabWords; i += NW * kWave) s_gtab[i] = kGeluTab[i];
-  }
-  FragReader<BM, kAK, TM, BK> fa;
-  FragReader<BN, kBKm, TN, BK> fb;
-  fa.init(wm * WM, lane);
-  fb.init(wn * WN, lane);
-
-  TileJob job;
-  setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, logical, job);
-  Loader ld;
-  ld.init(job, wave, lane);
-  int64_t nk = ceil_div(job.kred, BK);
-  Stage R0, R1;
-  if (nk > 0) R0.load(ld, 0);
-  if (nk > 1) R1.load(ld, 1);
-
-  typedef typename mfma_op<T>::vec vec;
-  f32x16_t acc[TM][TN];
-  auto compute = [&](const char* sa, const char* sb) {
-    vec av[2][TM], bv[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) av[0][i] = fa.template read<vec>(sa, i, 0);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bv[0][j] = fb.template read<vec>(sb, j, 0);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < BK / 16) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = fb.template read<vec>(sb, j, ks + 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_op<T>::run(bv[cur][j], av[cur][i], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  // Iteration kt: Rn holds stage kt+1 (loaded two iterations ago); it goes
-  // to the LDS slot not being read (its readers passed the last barrier),
-  // then receives stage kt+3; stage kt is multiplied from slot `cur`.
-  auto step = [&](int64_t kt, Stage& Rn, int cur) {
-    if (kt + 1 < nk) Rn.store(smem + (cur ^ 1) * kStage, wave, lane);
-    if (kt + 3 < nk) Rn.load(ld, kt + 3);
-    compute(smem + cur * kStage, smem + cur * kStage + Loader::TA::kBytes);
-    __syncthreads();
-  };
-
-  while (true) {
-    zero_acc<T>(acc);
-    // Stage 0 into slot 0 (the previous tile's epilogue used slot 1),
-    // stage 2 into R0.
-    if (nk > 0) R0.store(smem, wave, lane);
-    if (nk > 2) R0.load(ld, 2);
-    __syncthreads();
-    for (int64_t kt = 0; kt < nk; kt += 2) {
-      step(kt, R1, 0);
-      if (kt + 1 < nk) step(kt + 1, R0, 1);
-    }
-    // The next tile's first two stages load behind this tile's epilogue.
-    const int64_t next = logical + nbx;
-    const bool more = next < t_end;
-    TileJob nj;
-    if (more) {
-      setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, next, nj);
-      ld.init(nj, wave, lane);
-      nk = ceil_div(nj.kred, BK);
-      if (nk > 0) R0.load(ld, 0);
-      if (nk > 1) R1.load(ld, 1);
-    }
-    if (MODE == kDw && job.pf != nullptr) {
-      store_partial(acc, job, wm * WM, wn * WN, lane);
-    } else {
-      static_assert(NW * epi_bytes<TN, 32>() <= kStage, "epilogue scratch fits one slot");
-      store_tile_lds<T, EPI, kTab, 32>(acc, job, wm * WM, wn * WN, lane,
-                                       smem + kStage + wave * epi_bytes<TN, 32>(), s_gtab);
     }
     if (!more) break;
     job = nj;
@@ -1516,14 +1481,14 @@ int blocks_per_cu(K kernel, int threads) {
   return n;
 }
 
-template <int MODE, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS>
+template <int MODE, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false>
 int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t tiles = plan_tiles<MODE>(g, out_cols, BM, EPI == kEpiSwiGLU ? BN / 2 : BN);
   if (tiles == 0) return NT_OK;
   if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
   constexpr int threads = WGM * WGN * kWave;
-  auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS, EPI>;
-  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS, EPI>;
+  auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>;
+  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>;
   // Occupancy of this instantiation (bf16 and fp16 share resource usage).
   static const int per_cu = blocks_per_cu(kb, threads);
   // Persistent: at most one resident wave of workgroups; each walks tiles.
@@ -1536,27 +1501,13 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   return launch_status();
 }
 
-// The 4-wave register-staged kernel (256x256 tiles, one workgroup per CU).
-template <int MODE, int EPI>
-int launch_mfma4(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
-  const int64_t tiles = plan_tiles<MODE>(g, out_cols, 256, 256);
-  if (tiles == 0) return NT_OK;
-  if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
-  auto kb = gg_mfma4_kernel<bf16, MODE, EPI>;
-  auto kh = gg_mfma4_kernel<f16, MODE, EPI>;
-  static const int per_cu = blocks_per_cu(kb, 256);
-  const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
-  const dim3 grid((unsigned)nblocks);
-  if (dtype == NT_BF16)
-    hipLaunchKernelGGL(kb, grid, dim3(256), 0, s, g);
-  else
-    hipLaunchKernelGGL(kh, grid, dim3(256), 0, s, g);
-  return launch_status();
-}
-
 // Tile shape (measured on MI355X over the configs' shapes): 256x256 with 8
 // waves unless that leaves fewer than 1.5 tiles per CU, then 128x128 with 4
-// waves (two workgroups per CU).
+// waves (two workgroups per CU). Plain 256x256 forward / dX tiles with a
+// reduction of at least kSplitMinRed split load and store duties between the
+// waves (measured: C4 +5%, C2 down-projection -10 us; shorter reductions and
+// the GELU epilogue were slower split).
+constexpr int64_t kSplitMinRed = 1024;
 template <int MODE, int EPI>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t chunks = g.chunk > 0 ? g.E + g.A / g.chunk : g.E;
@@ -1569,8 +1520,14 @@ int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
     (void)tiles256;
     return launch_mfma<MODE, EPI, 256, 256, 4, 2, 64, 2>(dtype, g, out_cols, s);
   } else {
-    if (tiles256 * 2 >= (int64_t)device_cus() * 3)
+    if (tiles256 * 2 >= (int64_t)device_cus() * 3) {
+      if constexpr (MODE != kDw && (EPI == kEpiPlain || EPI == kEpiDualK)) {
+        const int64_t red = MODE == kFwd ? g.K : (EPI == kEpiDualK ? 2 * g.N : g.N);
+        if (red >= kSplitMinRed)
+          return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2, true>(dtype, g, out_cols, s);
+      }
       return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
+    }
     return launch_mfma<MODE, EPI, 128, 128, 2, 2, 64, 2>(dtype, g, out_cols, s);
   }
 }
