@@ -206,16 +206,33 @@ def cpu_baseline(cfg_id: int, budget_s: float = 20.0):
     cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     torch.set_num_threads(cores)
-    T = min(T0, 4096)
-    wl = make_workload(cfg_id, "cpu", seed=99, T=T)
-    weights = {"up": wl["W_up"], "down": wl["W_down"]}
+
+    def layer(wl):
+        weights = {"up": wl["W_up"], "down": wl["W_down"]}
+        O.moe_layer_torch(wl["X"], wl["logits"], weights, k, ffn="gelu", dY=wl["dY"])
+
+    # Size the sample from a 256-token probe so that warmup + timed
+    # iterations stay near budget_s (fp16 on the CPU is slow at C5).
+    T = min(T0, 256)
+    probe = make_workload(cfg_id, "cpu", seed=99, T=T)
+    layer(probe)
     t0 = time.perf_counter()
-    O.moe_layer_torch(wl["X"], wl["logits"], weights, k, ffn="gelu", dY=wl["dY"])  # warmup
-    first = time.perf_counter() - t0
+    layer(probe)
+    per_token = (time.perf_counter() - t0) / T
+    T = int(min(T0, 4096, max(256, budget_s / 4 / per_token)) // 256 * 256)
+    print(f"bench.py: cpu_baseline sample {T} tokens (~{per_token * T:.1f} s per iteration)",
+          file=sys.stderr, flush=True)
+    if T == probe["T"]:
+        wl, first = probe, per_token * T  # the probe runs were the warmup
+    else:
+        wl = make_workload(cfg_id, "cpu", seed=99, T=T)
+        t0 = time.perf_counter()
+        layer(wl)  # warmup
+        first = time.perf_counter() - t0
     iters = max(1, min(3, int(budget_s / max(first, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(iters):
-        O.moe_layer_torch(wl["X"], wl["logits"], weights, k, ffn="gelu", dY=wl["dY"])
+        layer(wl)
     dt = (time.perf_counter() - t0) / iters
     return {
         "value": T / dt,
