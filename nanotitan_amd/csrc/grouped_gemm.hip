@@ -685,24 +685,32 @@ __device__ __forceinline__ void gelu2_formula(uint32_t w, uint32_t& r, uint32_t&
 // outside that range take the erfc fit.
 __device__ __forceinline__ void gelu8_table(const uint32_t (&w)[4], const uint32_t* tab,
                                             uint32_t (&r)[4], uint32_t (&r2)[4]) {
-  uint32_t a[8], t[8];
+  // Both halves of a word at once (packed 16-bit integer ops): entry
+  // m = |x| - kGeluTabLo (clamped), byte offset 8m + 4*sign.
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const char* tb = reinterpret_cast<const char*>(tab);
+  uint32_t t[8];
   bool out = false;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t e = (i & 1) ? w[i / 2] >> 16 : w[i / 2] & 0xffffu;
-    a[i] = (e & 0x7fffu) - kGeluTabLo;  // wraps to a large value below the range
-    out |= a[i] >= kGeluTabN;
-    t[i] = tab[2 * min(a[i], kGeluTabN - 1) + (e >> 15)];
+  for (int q = 0; q < 4; ++q) {
+    const u16x2 x = __builtin_bit_cast(u16x2, w[q]);
+    const u16x2 a = (x & (u16x2)0x7fff) - (u16x2)kGeluTabLo;  // wraps below the range
+    const u16x2 m = __builtin_elementwise_min(a, (u16x2)(kGeluTabN - 1));
+    out |= __builtin_bit_cast(uint32_t, a) != __builtin_bit_cast(uint32_t, m);
+    const uint32_t o = __builtin_bit_cast(uint32_t, (u16x2)((m << 3) | ((x >> 13) & (u16x2)4)));
+    t[2 * q] = *reinterpret_cast<const uint32_t*>(tb + (o & 0xffffu));
+    t[2 * q + 1] = *reinterpret_cast<const uint32_t*>(tb + (o >> 16));
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    r[q] = (t[2 * q] & 0xffffu) | (t[2 * q + 1] << 16);
-    r2[q] = (t[2 * q] >> 16) | (t[2 * q + 1] & 0xffff0000u);
+    r[q] = __builtin_amdgcn_perm(t[2 * q + 1], t[2 * q], 0x05040100u);   // low halves
+    r2[q] = __builtin_amdgcn_perm(t[2 * q + 1], t[2 * q], 0x07060302u);  // high halves
   }
   if (out) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bool o0 = a[2 * q] >= kGeluTabN, o1 = a[2 * q + 1] >= kGeluTabN;
+      const bool o0 = (w[q] & 0x7fffu) - kGeluTabLo >= kGeluTabN;
+      const bool o1 = ((w[q] >> 16) & 0x7fffu) - kGeluTabLo >= kGeluTabN;
       if (o0 || o1) {
         uint32_t f, f2;
         gelu2_formula<bf16>(w[q], f, f2);
@@ -1623,6 +1631,13 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
                  typename elem<T>::storage* __restrict__ dW) {
   __shared__ int32_t s_info[2];
   const int e = blockIdx.y;
+  {
+    // Experts in one chunk were written by the GEMM: leave before the
+    // prefix (the common case for balanced routing). Uniform per block.
+    int64_t a, b;
+    expert_rows(offsets, e, A, a, b);
+    if (dw_chunks(b - a, R) < 2) return;
+  }
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
     int before = 0;

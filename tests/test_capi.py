@@ -86,6 +86,13 @@ def test_workspace_sizes_are_sane():
          capi.NT_ERR_INVALID_ARG),
         ("nt_route_topk_count", (None, 8, 1025, 2, None, None, None, 16, None, None),
          capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_route_topk_count", (None, 8, 4, 2, None, None, None, 24, None, None),
+         capi.NT_ERR_INVALID_ARG),  # block size not a power of two
+        ("nt_route_topk", (None, 8, 1025, 2, None, None, None, None), capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_route_topk_backward", (None, None, None, 8, 1025, 2, None, None),
+         capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_route_topk_backward", (None, None, None, 8, 64, 33, None, None),
+         capi.NT_ERR_INVALID_ARG),
         ("nt_dispatch_counted", (capi.NT_BF16, None, None, None, 8, 2, 16, 1025, None, None,
                                  None, None, None, None, None, None, 0, None),
          capi.NT_ERR_TOO_MANY_EXPERTS),

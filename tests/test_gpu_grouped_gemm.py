@@ -177,3 +177,39 @@ def test_dw_split_reduction_for_skewed_experts(ext, dtype, counts):
     for e, n in enumerate(counts):
         if n == 0:
             assert not a[e].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K,N", [(1032, 1000), (1000, 1032)])
+def test_split_duty_tiles_ragged(ext, dtype, K, N):
+    """Shapes large enough for 256x256 tiles with split load/store duties
+    (at least 1.5 tiles per CU, reduction >= 1024): uneven experts (tiles
+    cross expert ends), output columns and the reduction not multiples of
+    the tile, for forward, dX and the two-part dX."""
+    counts = [6000, 0, 9777, 3, 13220]
+    A = sum(counts)
+    # the launcher's rule: ceil(A/256) * ceil(out_cols/256) >= 1.5 tiles per CU
+    tiles = -(-A // 256) * -(-min(K, N) // 256)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert 2 * tiles >= 3 * cus, "shape too small to reach the 256x256 split path"
+    g = torch.Generator().manual_seed(K * 7 + N)
+    offsets = torch.zeros(len(counts) + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    E = len(counts)
+    X = torch.randn(A, K, generator=g).to(dtype)
+    W = (torch.randn(E, K, N, generator=g) / K ** 0.5).to(dtype)
+    W2 = (torch.randn(E, K, N, generator=g) / K ** 0.5).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    G2 = torch.randn(A, N, generator=g).to(dtype)
+    Xg, Wg, W2g, og, Gg, G2g = X.cuda(), W.cuda(), W2.cuda(), offsets.cuda(), G.cuda(), G2.cuda()
+    out = ext.grouped_gemm_kernel(Xg, og, Wg)
+    dX = ext.bwd_grouped_gemm_dX_kernel(Wg, og, Gg)
+    dX2 = ext.bwd_grouped_gemm_dX2(Wg, W2g, og, Gg, G2g)
+    torch.cuda.synchronize()
+    check(out, O.grouped_gemm(X, offsets, W), dtype)
+    want_dx = O.grouped_gemm_dx(W, offsets, G)
+    check(dX, want_dx, dtype, scale=(N / K) ** 0.5)
+    check(dX2, want_dx + O.grouped_gemm_dx(W2, offsets, G2), dtype, scale=(2 * N / K) ** 0.5)
+    # deterministic, and rows past the experts' end untouched by neighbours
+    again = ext.grouped_gemm_kernel(Xg, og, Wg)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
