@@ -57,15 +57,18 @@ __host__ __device__ inline RouterLayout router_layout(int32_t E) {
 }
 
 // Selection order as one unsigned 64-bit key, larger = chosen first: the
-// high word maps the float to an unsigned integer of the same order (sign
-// flipped; -0 taken as +0 so the two tie; every NaN maps to 0, below -inf),
+// high word maps the float's bits to an unsigned integer of the same order
+// (sign flipped; -0 taken as +0 so the two tie; every NaN maps to 0, below
+// -inf),
 // the low word is ~expert so equal values go to the lower expert id. Key 0
 // marks an empty slot (padding or already taken): it ranks below every
 // expert, NaNs included, since ~e >= 2^31 for e < 2^31.
 __device__ __forceinline__ uint64_t order_key(float x, int e) {
-  const float f = x + 0.0f;  // -0 -> +0
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t hi = (f != f) ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+  // Integer-only, so denormals keep their order whatever the float mode.
+  uint32_t u = __float_as_uint(x);
+  if (u == 0x80000000u) u = 0u;  // -0 -> +0
+  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  const uint32_t hi = nan ? 0u : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
   return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)e;
 }
 

@@ -73,3 +73,28 @@ def test_route_rejects_bad_k(ext):
         ext.route_topk(torch.zeros(4, 8, device="cuda"), 9)
     with pytest.raises(RuntimeError):
         ext.route_topk(torch.zeros(4, 64, device="cuda"), 33)
+
+
+def test_route_special_values(ext):
+    """Signed zeros tie (lower id first), denormals keep their order, +-FLT_MAX
+    and +-inf rank at the ends: indices equal the oracle's stable descending
+    sort; gates compared where the selected logits are finite."""
+    tiny = 1e-45  # smallest fp32 denormal
+    big = 3.4028234663852886e38
+    rows = [
+        [0.0, -0.0, -1.0, 1.0, -0.0, 0.0, 2.0, -2.0],
+        [-0.0, 0.0, 0.0, -0.0, -0.0, 0.0, -0.0, 0.0],
+        [tiny, 2 * tiny, -tiny, 0.0, -2 * tiny, 3 * tiny, -0.0, tiny],
+        [big, -big, 1.0, big, -big, 0.0, -1.0, 5.0],
+        [float("-inf"), -1.0, float("-inf"), 0.5, float("-inf"), -3.0, float("-inf"), 0.25],
+        [float("inf"), 1.0, float("-inf"), 0.0, 2.0, float("inf"), -1.0, 3.0],
+    ]
+    logits = torch.tensor(rows, dtype=torch.float32).repeat(50, 1)  # several per wave
+    for k in (1, 3, 5, 8):
+        want_g, want_i, _ = O.route(logits, k)
+        g, i = ext.route_topk(logits.cuda(), k)
+        torch.cuda.synchronize()
+        assert np.array_equal(i.cpu().numpy(), want_i.numpy()), k
+        fin = torch.isfinite(want_g).all(dim=1)  # rows with +inf selected have NaN gates
+        assert fin.sum() >= 4 * 50
+        torch.testing.assert_close(g.cpu()[fin], want_g[fin], rtol=2e-6, atol=1e-7)
