@@ -908,45 +908,38 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
   }
 }
 
-// Epilogue of the 8-wave kernel with split duties: waves NW/2..NW-1 issue
-// every global store of the tile and never wait for them, so the stores
-// drain behind the next tile's k-loop (vmcnt is per wave and retires in
-// issue order: a wave that also issued the operand loads would wait for its
-// stores at its next load wait). Each round every wave rounds a 16-row half
-// of one of its 32-row sub-tiles into its LDS scratch region (applying GELU
-// there for kEpiGelu, so that VALU work stays spread over all waves; the
-// launcher uses the split for plain epilogues only); after
-// a barrier storer wave w reads back its own region and that of wave
-// w - NW/2 (16 bytes per lane, whole 128-byte row segments) and stores both;
-// a second barrier frees the scratch for the next round. `scratch` holds
-// NW * kOuts * 16 * epi_pitch<TN>() bytes.
-template <int EPI, int TN>
+// Epilogue of the 8-wave kernel with split duties (plain and two-part
+// epilogues): waves NW/2..NW-1 issue every global store of the tile and
+// never wait for them, so the stores drain behind the next tile's k-loop
+// (vmcnt is per wave and retires in issue order: a wave that also issued the
+// operand loads would wait for its stores at its next load wait). Each round
+// every wave rounds a 16-row half of one of its 32-row sub-tiles into its LDS
+// scratch region; after a barrier storer wave w reads back its own region
+// and that of wave w - NW/2 (16 bytes per lane, whole 128-byte row segments)
+// and stores both; a second barrier frees the scratch for the next round.
+// `scratch` holds split_scratch_bytes<TN>(NW) bytes.
+template <int TN>
 constexpr int split_scratch_bytes(int nw) {
-  return nw * (EPI == kEpiGelu ? 2 : 1) * 16 * epi_pitch<TN>();
+  return nw * 16 * epi_pitch<TN>();
 }
-template <typename T, int EPI, bool TAB, int TM, int TN, int WGN, int WM, int WN, int NW>
+template <typename T, int TM, int TN, int WGN, int WM, int WN, int NW>
 __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], const TileJob& j,
-                                                 int wave, int lane, char* scratch,
-                                                 const uint32_t* tab) {
+                                                 int wave, int lane, char* scratch) {
   static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
-  static_assert(EPI == kEpiPlain || EPI == kEpiDualK || EPI == kEpiGelu,
-                "stores without epilogue inputs");
   constexpr int ROWS = 16;
-  constexpr int kOuts = EPI == kEpiGelu ? 2 : 1;
   constexpr int kPitch = epi_pitch<TN>();
-  constexpr int kRegion = ROWS * kPitch;  // one wave, one output
+  constexpr int kRegion = ROWS * kPitch;  // one wave's half sub-tile
   constexpr int kLanesPerRow = TN * 4;
   constexpr int kRowsPerRead = 64 / kLanesPerRow;
   constexpr int kQ = ROWS / kRowsPerRead;
   constexpr int NL = NW / 2;
   const bool storer = wave >= NL;
-  // In-tile bounds and offsets fit 32 bits (m < BM, ldo < 2^22).
+  // In-tile bounds and offsets fit 32 bits (m < 256, ldo < 2^22).
   const int rv = (int)(j.rows_valid < 256 ? j.rows_valid : 256);
   const int cv = (int)(j.cols_valid < 256 ? j.cols_valid : 256);
   const uint32_t ldo = (uint32_t)j.ldo;
-  char* mine = scratch + wave * kOuts * kRegion;
+  char* mine = scratch + wave * kRegion;
   const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
-  const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(kOuts == 2 ? j.po2 : j.po);
   const int r = lane & 31;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -957,35 +950,11 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-          for (int gp = 0; gp < 2; ++gp) {
-            // two 4-column groups (gq = 2gp, 2gp+1) of sub-tile (i, jn)
-            uint32_t w[4];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const int gq = 2 * gp + h;
-              w[2 * h] = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
-              w[2 * h + 1] = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
-            }
-            uint32_t o[4], o2[4];
-            if constexpr (EPI == kEpiGelu) {
-              if constexpr (TAB) {
-                gelu8_table(w, tab, o, o2);
-              } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) gelu2_formula<T>(w[q], o[q], o2[q]);
-              }
-            } else {
-#pragma unroll
-              for (int q = 0; q < 4; ++q) o[q] = w[q];
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const int c = jn * 32 + 8 * (2 * gp + h) + 4 * (lane >> 5);
-              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(o[2 * h], o[2 * h + 1]);
-              if constexpr (kOuts == 2)
-                *reinterpret_cast<uint2*>(row + kRegion + c * 2) =
-                    make_uint2(o2[2 * h], o2[2 * h + 1]);
-            }
+          for (int gq = 0; gq < 4; ++gq) {
+            const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
+            *reinterpret_cast<uint2*>(row + c * 2) =
+                make_uint2(pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]),
+                           pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]));
           }
       }
       __syncthreads();
@@ -995,7 +964,7 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
           const int src = h == 0 ? wave - NL : wave;
           const int sm0 = (src / WGN) * WM + i * 32 + ps * ROWS;
           const int sn0 = (src % WGN) * WN;
-          const char* sp = scratch + src * kOuts * kRegion;
+          const char* sp = scratch + src * kRegion;
 #pragma unroll
           for (int q = 0; q < kQ; ++q) {
             const int rr = q * kRowsPerRead + lane / kLanesPerRow;
@@ -1005,9 +974,6 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
             const uint32_t off =
                 (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
             store16(ro, off, *reinterpret_cast<const uint4*>(sp + rr * kPitch + ch * 16));
-            if constexpr (kOuts == 2)
-              store16(ro2, off,
-                      *reinterpret_cast<const uint4*>(sp + kRegion + rr * kPitch + ch * 16));
           }
         }
       }
@@ -1291,9 +1257,8 @@ gg_mfma_kernel(GemmArgs g) {
       store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
       stores_out = kDrain && more;
     } else if constexpr (kSplit) {
-      static_assert(split_scratch_bytes<EPI, TN>(NW) <= kStage, "split scratch fits one stage");
-      store_tile_split<T, EPI, kTab, TM, TN, WGN, WM, WN, NW>(acc, job, wave, lane,
-                                                             smem + (NS - 1) * kStage, s_gtab);
+      static_assert(split_scratch_bytes<TN>(NW) <= kStage, "split scratch fits one stage");
+      store_tile_split<T, TM, TN, WGN, WM, WN, NW>(acc, job, wave, lane, smem + (NS - 1) * kStage);
     } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
