@@ -86,6 +86,8 @@ class LaunchTimer:
         "bwd_grouped_gemm_dX_kernel": "gemm",
         "bwd_grouped_gemm_dX_gelu": "gemm",
         "bwd_grouped_gemm_dW_kernel": "gemm",
+        "bwd_grouped_gemm_dW_dX": "gemm",
+        "bwd_grouped_gemm_dW_dX_gelu": "gemm",
         "dispatch_tokens": "dispatch",
         "combine_inv": "combine_fwd",
         "combine_backward_inv": "combine_bwd",
@@ -111,10 +113,16 @@ class LaunchTimer:
             s.record()
             out = fn(*args)
             e.record()
-            self.records.append((fam, name, s, e, self._work(name, args)))
+            self.records.append((fam, name, s, e, self._work(name, args), self._launches(name)))
             return out
 
         return timed
+
+    @staticmethod
+    def _launches(name):
+        """GEMM launches inside one call (the paired dW + dX calls hold two,
+        which may run side by side: the pair's span is their joint time)."""
+        return 2 if name in ("bwd_grouped_gemm_dW_dX", "bwd_grouped_gemm_dW_dX_gelu") else 1
 
     @staticmethod
     def _work(name, args):
@@ -128,6 +136,9 @@ class LaunchTimer:
         if name == "bwd_grouped_gemm_dW_kernel":
             X, _off, G = args
             return 2.0 * X.shape[0] * X.shape[1] * G.shape[1]
+        if name in ("bwd_grouped_gemm_dW_dX", "bwd_grouped_gemm_dW_dX_gelu"):
+            X, _W, _off, G = args[:4]
+            return 2 * 2.0 * X.shape[0] * X.shape[1] * G.shape[1]
         if name == "dispatch_tokens":  # read X once, write packed rows, ids/gates
             X, w, topk, _E = args
             T, d = X.shape
@@ -154,10 +165,10 @@ class LaunchTimer:
 
     def summary(self):
         out = {}
-        for fam, name, s, e, work in self.records:
+        for fam, name, s, e, work, launches in self.records:
             ms = s.elapsed_time(e)
             r = out.setdefault(fam, {"launches": 0, "ms": 0.0, "work": 0.0})
-            r["launches"] += 1
+            r["launches"] += launches
             r["ms"] += ms
             r["work"] += work
         return out
@@ -338,7 +349,8 @@ def main():
         "flops_per_launch": gemm["work"] / max(gemm["launches"], 1),
         "avg_launch_ms": gemm["ms"] / max(gemm["launches"], 1),
         "timing": f"HIP events around each launch, second pass of the {args.steps} steps "
-                  f"({elapsed_events / args.steps * 1e3:.4f} ms/step with the events)",
+                  f"({elapsed_events / args.steps * 1e3:.4f} ms/step with the events); a paired "
+                  f"dW + dX call counts as two launches over its joint span",
     }
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
     # (calibrated on a device copy), committed with the profile summaries.

@@ -291,6 +291,29 @@ int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const v
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
                        size_t ws_bytes, hipStream_t stream);
 
+/* nt_grouped_gemm_dw (dW = X^T dOut, [E,K,N]) and nt_grouped_gemm_dx
+ * (dX = dOut W^T, [A,K]) in one call, for the backward of one expert
+ * projection: the two read the same dOut and are otherwise independent.
+ * When the dW has too few 256x256 tiles to fill the device and there are at
+ * most 16 experts, one kernel launch runs both side by side (the dW on
+ * 256x256 tiles, one per workgroup, the dX on the remaining CUs and then on
+ * the dW's as they finish); otherwise they run one after the other. Outputs are bit-identical to the two separate calls. ws: the dW
+ * workspace (nt_grouped_gemm_workspace_bytes). Replaces the pair of calls in
+ * GroupedGEMM_FN.backward (reference
+ * src/model/moe_ops.py:117-125; csrc/kernels/bwd_grouped_gemm_dW.cu:43-86,
+ * bwd_grouped_gemm_dX.cu:46-96). */
+int nt_grouped_gemm_dw_dx(int dtype, const void* X, const void* W, const int32_t* offsets,
+                          const void* dOut, int32_t E, int64_t A, int64_t K, int64_t N, void* dW,
+                          void* dX, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* The same pairing for the GELU FFN's down projection: dW = act^T dOut
+ * (nt_grouped_gemm_dw) and dH = (dOut W^T) * act_grad
+ * (nt_grouped_gemm_dx_gelu). act, act_grad [A,K]; W [E,K,N]; dOut [A,N]. */
+int nt_grouped_gemm_dw_dx_gelu(int dtype, const void* act, const void* W, const int32_t* offsets,
+                               const void* dOut, const void* act_grad, int32_t E, int64_t A,
+                               int64_t K, int64_t N, void* dW, void* dH, void* ws,
+                               size_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1028,10 +1028,31 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[TM][TN]) {
 // Tiles are dealt to XCDs in contiguous ranges (workgroup b runs on XCD
 // b % 8), so tiles that share operand panels share that XCD's L2; inside a
 // range, tile_coords walks groups of kGroupM m-tiles with m fastest.
+// LDS of one tile configuration (declared by the kernels that run it).
 template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
           bool SPLIT>
-__global__ void __launch_bounds__(WGM * WGN * kWave)
-gg_mfma_kernel(GemmArgs g) {
+struct GemmLds {
+  static constexpr int kDual = EPI == kEpiSwiGLU ? 1 : (EPI == kEpiDualK ? 2 : 0);
+  static constexpr int NL = SPLIT ? WGM * WGN / 2 : WGM * WGN;
+  typedef StageLoader<BM, BN, MODE != kDw, MODE == kDx, BK, NL, kDual> Loader;
+  static constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
+  static constexpr int kSmem = NS * kStage;
+  // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
+  static constexpr int kPref = (MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1);
+  // bf16 GELU epilogue of the 256-row tiles: the gelu / gelu' table in LDS
+  // (the 128-row tiles run two workgroups per CU, which the table would not
+  // leave room for).
+  static constexpr bool kTab = EPI == kEpiGelu && std::is_same<T, bf16>::value && BM == 256;
+  static constexpr int kTabWords = kTab ? kGeluTabWords : 1;
+};
+
+// The tile loop of workgroup `wg` of `G` that share this GEMM (the kernel's
+// body; gg_pair_kernel runs two of them side by side).
+template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
+          bool SPLIT, bool DYN = false>
+__device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_t G, char* smem,
+                                           int32_t* s_pref, uint32_t* s_gtab,
+                                           int32_t* dyn = nullptr, int64_t* s_next = nullptr) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -1053,14 +1074,7 @@ gg_mfma_kernel(GemmArgs g) {
   typedef StageLoader<BM, BN, kAK, kBKm, BK, NL, kDual> Loader;
   constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
   constexpr int kLoadsPerStage = Loader::kLoads;  // per loading wave
-  __shared__ __attribute__((aligned(1024))) char smem[NS * kStage];
-  // fwd / dX: m-tile prefix of the experts; dW: chunk prefix and split prefix.
-  __shared__ int32_t s_pref[(MODE == kDw ? 2 : 1) * (NT_MAX_EXPERTS + 1)];
-  // bf16 GELU epilogue of the 256-row tiles: the gelu / gelu' table in LDS
-  // (the 128-row tiles run two workgroups per CU, which the table would not
-  // leave room for).
-  constexpr bool kTab = EPI == kEpiGelu && std::is_same<T, bf16>::value && BM == 256;
-  __shared__ uint32_t s_gtab[kTab ? kGeluTabWords : 1];
+  constexpr bool kTab = GemmLds<T, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>::kTab;
 
   int64_t mtiles;
   if (MODE != kDw) {
@@ -1072,14 +1086,42 @@ gg_mfma_kernel(GemmArgs g) {
   }
   const int64_t total = mtiles * g.ntn;
   constexpr int kXcd = 8;
-  const int64_t G = gridDim.x;
-  const int xcd = blockIdx.x % kXcd;
+  const int xcd = (int)(wg % kXcd);
   const int64_t q = G / kXcd, r = G % kXcd;
   const int64_t before = xcd * q + (xcd < r ? xcd : r);
   const int64_t nbx = q + (xcd < r ? 1 : 0);  // workgroups on this XCD
   const int64_t t_end = total * (before + nbx) / G;
-  int64_t logical = total * before / G + blockIdx.x / kXcd;
-  if (logical >= t_end) return;
+  int64_t logical = total * before / G + wg / kXcd;
+  // Dynamic order (DYN): the tiles form kXcd contiguous parts;
+  // workgroup wg takes the next tile of its XCD's part from counter dyn[p]
+  // (zeroed before the launch), then those of the following parts. One
+  // thread claims, the LDS slot *s_next publishes it at a barrier.
+  auto claim = [&]() -> int64_t {
+    for (int i = 0; i < kXcd; ++i) {
+      const int p = (xcd + i) % kXcd;
+      const int64_t p0 = total * p / kXcd, p1 = total * (p + 1) / kXcd;
+      if (p1 <= p0) continue;
+      const int64_t c = atomicAdd(dyn + p, 1);
+      if (c < p1 - p0) return p0 + c;
+    }
+    return -1;
+  };
+  // The claimed index is the same for the whole workgroup: keep it scalar.
+  auto uniform = [](int64_t v) -> int64_t {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  if constexpr (DYN) {
+    if (threadIdx.x == 0) *s_next = claim();
+    __syncthreads();
+    logical = uniform(*s_next);
+    if (logical < 0) return;
+  } else {
+    (void)claim;
+    (void)uniform;
+    if (logical >= t_end) return;
+  }
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1203,9 +1245,13 @@ gg_mfma_kernel(GemmArgs g) {
     }
     // Every wave is done with the stages; start the next tile's loads, then
     // store this tile.
-    const int64_t next = logical + nbx;
-    const bool more = next < t_end;
+    int64_t next = logical + nbx;
+    if constexpr (DYN) {
+      if (threadIdx.x == 0) *s_next = claim();
+    }
     __syncthreads();
+    if constexpr (DYN) next = uniform(*s_next);
+    const bool more = DYN ? next >= 0 : next < t_end;
     TileJob nj;
     if (more) {
       setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, next, nj);
@@ -1273,6 +1319,48 @@ gg_mfma_kernel(GemmArgs g) {
     job = nj;
     logical = next;
   }
+}
+
+template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
+          bool SPLIT>
+__global__ void __launch_bounds__(WGM * WGN * kWave)
+gg_mfma_kernel(GemmArgs g) {
+  typedef GemmLds<T, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT> L;
+  __shared__ __attribute__((aligned(1024))) char smem[L::kSmem];
+  __shared__ int32_t s_pref[L::kPref];
+  __shared__ uint32_t s_gtab[L::kTabWords];
+  gemm_tiles<T, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>(g, blockIdx.x, gridDim.x, smem, s_pref,
+                                                           s_gtab);
+}
+
+// A dW and a dX-type GEMM in one launch, side by side: workgroups [0, nw)
+// walk the dW's tiles (gw, static ranges), then every workgroup takes dX
+// tiles (gx) in the dynamic order, so the workgroups that started on the dX
+// keep the device busy while the dW's run, and any imbalance in the dW (a
+// skewed expert's chunks) is absorbed. Both on 256x256 tiles with 8 waves;
+// nw is a multiple of 8, so the dW part keeps the XCD mapping (workgroup b
+// runs on XCD b % 8). dyn: kXcd zeroed counters.
+template <typename T, int EPIX, bool SPLITX>
+__global__ void __launch_bounds__(8 * kWave)
+gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, int32_t* dyn) {
+  typedef GemmLds<T, kDw, 256, 256, 2, 4, 64, 2, kEpiPlain, false> LW;
+  typedef GemmLds<T, kDx, 256, 256, 2, 4, 64, 2, EPIX, SPLITX> LX;
+  static_assert(!LX::kTab, "no GELU table in the pair kernel");
+  __shared__ __attribute__((aligned(1024))) char smem[LW::kSmem > LX::kSmem ? LW::kSmem : LX::kSmem];
+  __shared__ int32_t s_pref[LW::kPref > LX::kPref ? LW::kPref : LX::kPref];
+  __shared__ uint32_t s_gtab[1];
+  __shared__ int64_t s_next;
+  if ((int32_t)blockIdx.x < nw) {
+    gemm_tiles<T, kDw, 256, 256, 2, 4, 64, 2, kEpiPlain, false>(gw, blockIdx.x, nw, smem, s_pref,
+                                                               s_gtab);
+    __syncthreads();  // LDS is reused by the dX tiles below
+  }
+  gemm_tiles<T, kDx, 256, 256, 2, 4, 64, 2, EPIX, SPLITX, true>(gx, blockIdx.x, gridDim.x, smem,
+                                                              s_pref, s_gtab, dyn, &s_next);
+}
+
+__global__ void zero_i32_kernel(int32_t* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
 }
 
 // ------------------------------------------------------- generic FMA kernel
@@ -1661,6 +1749,9 @@ int32_t dw_chunk_rows(int64_t A, int64_t K, int64_t N, int32_t E) {
   if (R >= A) return 0;
   return (int32_t)R;
 }
+// Workspace of the dW entry points: kCtrBytes of tile counters (paired
+// launches), then the fp32 partial slabs of split experts.
+constexpr size_t kCtrBytes = 256;
 size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
   const int32_t R = dw_chunk_rows(A, K, N, E);
   if (R == 0) return 0;
@@ -1741,6 +1832,133 @@ int check_gemm(int dtype, int32_t E, int64_t A, int64_t K, int64_t N, const void
 }  // namespace
 }  // namespace nt
 
+namespace nt {
+namespace {
+
+// dX-type GEMM (plain, or with the GELU backward when act_grad is set) and
+// dW; the C entry points below wrap them.
+template <int EPI>
+int dx_impl(int dtype, const void* W, const int32_t* offsets, const void* dOut,
+            const void* act_grad, int32_t E, int64_t A, int64_t K, int64_t N, void* dX,
+            hipStream_t stream) {
+  if (A == 0 || K == 0) return NT_OK;
+  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, act_grad, 0, nullptr};
+  bool mfma = mfma_ok(dtype, K, N, dOut, W, dX);
+  if (EPI == kEpiGeluGrad) mfma = mfma && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
+  return launch_mode<kDx, EPI>(dtype, g, K, mfma, stream);
+}
+
+int launch_dw_reduce(int dtype, const int32_t* offsets, int32_t E, int64_t A, int64_t K,
+                     int64_t N, int32_t R, const float* partial, void* dW, hipStream_t stream) {
+  const int64_t KN = K * N;
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(KN, 256 * 8), 64), (unsigned)E);
+  if (dtype == NT_BF16)
+    hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, R,
+                       partial, KN, static_cast<uint16_t*>(dW));
+  else
+    hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, R,
+                       partial, KN, static_cast<uint16_t*>(dW));
+  return launch_status();
+}
+
+int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, int32_t E,
+            int64_t A, int64_t K, int64_t N, void* dW, void* ws, size_t ws_bytes,
+            hipStream_t stream) {
+  if (K == 0 || N == 0) return NT_OK;
+  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
+  const bool mfma = mfma_ok(dtype, K, N, X, dOut, dW);
+  // Split long reductions (skewed experts) when the caller's workspace holds
+  // the partial slabs; without it every expert is one chunk.
+  const int32_t R = mfma ? dw_chunk_rows(A, K, N, E) : 0;
+  const bool split = R > 0 && ws != nullptr && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E) &&
+                     reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+  float* partial = split ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCtrBytes) : nullptr;
+  if (split) {
+    g.chunk = R;
+    g.partial = partial;
+  }
+  int st = launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma, stream);
+  if (st != NT_OK || !split) return st;
+  return launch_dw_reduce(dtype, offsets, E, A, K, N, R, partial, dW, stream);
+}
+
+// dW = X^T dOut and a dX-type GEMM (gx, epilogue EPIX) over the same
+// (A, K, N), which share nothing but their inputs. When the dW alone has too
+// few 256x256 tiles to fill the device (it would run on 128x128 tiles, at
+// about two thirds of the per-CU rate), both run in one launch of
+// gg_pair_kernel: the dW on 256x256 tiles, one per workgroup, and the dX's
+// tiles on the remaining workgroups, which the dW's workgroups join when
+// their own tiles are done (gg_pair_kernel). Measured at C2: 358 -> 309 us
+// with the GELU backward, 271 -> 245 us without. Results are bit-identical
+// to the two separate calls (every output tile is reduced in the same
+// order).
+constexpr int32_t kPairMaxExperts = 16;
+
+template <int EPIX>
+int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOut, int32_t E,
+               int64_t A, int64_t K, int64_t N, void* dW, void* ws, size_t ws_bytes,
+               GemmArgs gx, bool dx_mfma, hipStream_t stream) {
+  const int64_t cus = device_cus();
+  const bool mfma_dw = mfma_ok(dtype, K, N, X, dOut, dW);
+  const int32_t R = mfma_dw ? dw_chunk_rows(A, K, N, E) : 0;
+  const bool aligned = ws != nullptr && reinterpret_cast<uintptr_t>(ws) % 16 == 0;
+  const bool split = R > 0 && aligned && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E);
+  // Workgroups for the dW: one per tile of the experts' full reductions. A
+  // skewed expert split into chunks adds tiles that the same workgroups
+  // walk (the persistent loop counts the tiles on the device); sizing for
+  // the host's upper bound on chunks would leave workgroups idle.
+  const int64_t dw_tiles = (int64_t)E * ceil_div(K, 256) * ceil_div(N, 256);
+  const int64_t nw = round_up(dw_tiles, 8);
+  // Few experts only: with many (C3: 64, Zipf-skewed) the total work is
+  // small next to one 256x256 dW tile over a whole chunk of a heavy expert,
+  // which then becomes the critical path (measured: C3 1.37 -> 1.53 ms per
+  // layer step paired), while 128x128 tiles balance it.
+  const bool pair = mfma_dw && dx_mfma && A > 0 && K > 0 && N > 0 && aligned &&
+                    ws_bytes >= kCtrBytes && E <= kPairMaxExperts && dw_tiles * 2 < cus * 3 &&
+                    nw <= cus - cus / 4 && cus % 8 == 0;
+  if (!pair) {
+    const int st = dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+    if (st != NT_OK) return st;
+    return launch_mode<kDx, EPIX>(dtype, gx, K, dx_mfma, stream);
+  }
+  GemmArgs gw{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
+  float* partial = split ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCtrBytes) : nullptr;
+  if (split) {
+    gw.chunk = R;
+    gw.partial = partial;
+  }
+  int32_t* dyn = static_cast<int32_t*>(ws);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(kWave), 0, stream, dyn, 8);
+  plan_tiles<kDw>(gw, N, 256, 256);
+  plan_tiles<kDx>(gx, K, 256, 256);
+  constexpr bool kPlain = EPIX == kEpiPlain;
+  const bool splitx = kPlain && N >= kSplitMinRed;
+  const dim3 grid((unsigned)cus);
+  const dim3 block(8 * kWave);
+  const int32_t nw32 = (int32_t)nw;
+  if (dtype == NT_BF16) {
+    if (splitx) {
+      if constexpr (kPlain)
+        hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn);
+    } else {
+      hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn);
+    }
+  } else {
+    if (splitx) {
+      if constexpr (kPlain)
+        hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn);
+    } else {
+      hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn);
+    }
+  }
+  int st = launch_status();
+  if (st != NT_OK || !split) return st;
+  return launch_dw_reduce(dtype, offsets, E, A, K, N, R, partial, dW, stream);
+}
+
+}  // namespace
+}  // namespace nt
+
 using namespace nt;
 
 extern "C" {
@@ -1748,7 +1966,7 @@ extern "C" {
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N) {
   if (dtype != NT_BF16 && dtype != NT_F16) return 0;
   if (E < 1 || A < 0 || K < 0 || N < 0) return 0;
-  return dw_ws_bytes(A, K, N, E);
+  return kCtrBytes + dw_ws_bytes(A, K, N, E);
 }
 
 int nt_grouped_gemm(int dtype, const void* X, const int32_t* offsets, const void* W, int32_t E,
@@ -1785,9 +2003,7 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
   (void)ws_bytes;
   int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
   if (st != NT_OK) return st;
-  if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr};
-  return launch_mode<kDx, kEpiPlain>(dtype, g, K, mfma_ok(dtype, K, N, dOut, W, dX), stream);
+  return dx_impl<kEpiPlain>(dtype, W, offsets, dOut, nullptr, E, A, K, N, dX, stream);
 }
 
 int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, const void* dOut,
@@ -1798,11 +2014,7 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
   int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH);
   if (st != NT_OK) return st;
   if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
-  if (A == 0 || K == 0) return NT_OK;
-  GemmArgs g{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad, 0, nullptr};
-  const bool mfma =
-      mfma_ok(dtype, K, N, dOut, W, dH) && reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
-  return launch_mode<kDx, kEpiGeluGrad>(dtype, g, K, mfma, stream);
+  return dx_impl<kEpiGeluGrad>(dtype, W, offsets, dOut, act_grad, E, A, K, N, dH, stream);
 }
 
 int nt_grouped_gemm_swiglu(int dtype, const void* X, const int32_t* offsets, const void* W_gate,
@@ -1865,29 +2077,38 @@ int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const v
                        size_t ws_bytes, hipStream_t stream) {
   int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
   if (st != NT_OK) return st;
-  if (K == 0 || N == 0) return NT_OK;
-  GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
-  const bool mfma = mfma_ok(dtype, K, N, X, dOut, dW);
-  // Split long reductions (skewed experts) when the caller's workspace holds
-  // the partial slabs; without it every expert is one chunk.
-  const int32_t R = mfma ? dw_chunk_rows(A, K, N, E) : 0;
-  const bool split = R > 0 && ws != nullptr && ws_bytes >= dw_ws_bytes(A, K, N, E) &&
-                     reinterpret_cast<uintptr_t>(ws) % 16 == 0;
-  if (split) {
-    g.chunk = R;
-    g.partial = static_cast<float*>(ws);
-  }
-  st = launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma, stream);
-  if (st != NT_OK || !split) return st;
-  const int64_t KN = K * N;
-  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(KN, 256 * 8), 64), (unsigned)E);
-  if (dtype == NT_BF16)
-    hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, R,
-                       static_cast<const float*>(ws), KN, static_cast<uint16_t*>(dW));
-  else
-    hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, R,
-                       static_cast<const float*>(ws), KN, static_cast<uint16_t*>(dW));
-  return launch_status();
+  return dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+}
+
+int nt_grouped_gemm_dw_dx(int dtype, const void* X, const void* W, const int32_t* offsets,
+                          const void* dOut, int32_t E, int64_t A, int64_t K, int64_t N, void* dW,
+                          void* dX, void* ws, size_t ws_bytes, hipStream_t stream) {
+  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
+  if (st != NT_OK) return st;
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
+  if (st != NT_OK) return st;
+  if (A == 0 || K == 0) return dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  GemmArgs gx{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr};
+  return pair_dw_dx<kEpiPlain>(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, gx,
+                               mfma_ok(dtype, K, N, dOut, W, dX), stream);
+}
+
+int nt_grouped_gemm_dw_dx_gelu(int dtype, const void* act, const void* W, const int32_t* offsets,
+                               const void* dOut, const void* act_grad, int32_t E, int64_t A,
+                               int64_t K, int64_t N, void* dW, void* dH, void* ws,
+                               size_t ws_bytes, hipStream_t stream) {
+  int st = check_gemm(dtype, E, A, K, N, act, dOut, offsets, dW);
+  if (st != NT_OK) return st;
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH);
+  if (st != NT_OK) return st;
+  if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0)
+    return dw_impl(dtype, act, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  GemmArgs gx{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad, 0, nullptr};
+  const bool dx_mfma = mfma_ok(dtype, K, N, dOut, W, dH) &&
+                       reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;
+  return pair_dw_dx<kEpiGeluGrad>(dtype, act, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, gx,
+                                  dx_mfma, stream);
 }
 
 }  // extern "C"

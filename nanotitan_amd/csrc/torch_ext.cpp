@@ -327,6 +327,60 @@ Tensor bwd_grouped_gemm_dX_gelu(Tensor W, Tensor offsets, Tensor dOut, Tensor ac
   return dH;
 }
 
+// bwd_grouped_gemm_dW_dX(X, W, expert_offset, dOut) -> (dW [E,K,N], dX [A,K]):
+// the dW and dX of one projection in one call (a dW with few tiles runs
+// beside the dX in the same kernel launch).
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX(Tensor X, Tensor W, Tensor offsets, Tensor dOut) {
+  check_gemm_inputs(X, offsets, dOut);
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(X.dim() == 2 && W.dim() == 3 && dOut.dim() == 2 && dOut.size(0) == X.size(0) &&
+                  W.size(1) == X.size(1) && W.size(2) == dOut.size(1),
+              "expected X [A,K], W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = X.size(0), K = X.size(1), N = dOut.size(1);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor dW = at::empty({E, K, N}, X.options());
+  Tensor dX = at::empty({A, K}, X.options());
+  const int dt = dtype_code(X);
+  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dw_dx(dt, X.data_ptr(), W.data_ptr(), offsets.data_ptr<int32_t>(),
+                                     dOut.data_ptr(), E, A, K, N, dW.data_ptr(), dX.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), stream_of(X)),
+               "bwd_grouped_gemm_dW_dX");
+  return {dW, dX};
+}
+
+// bwd_grouped_gemm_dW_dX_gelu(act, W, expert_offset, dOut, act_grad) -> (dW, dH):
+// bwd_grouped_gemm_dW_kernel(act, ., dOut) and bwd_grouped_gemm_dX_gelu(W, ., dOut,
+// act_grad) in one call, paired like bwd_grouped_gemm_dW_dX.
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX_gelu(Tensor act, Tensor W, Tensor offsets,
+                                                       Tensor dOut, Tensor act_grad) {
+  check_gemm_inputs(act, offsets, dOut);
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(act.dim() == 2 && W.dim() == 3 && dOut.dim() == 2 && dOut.size(0) == act.size(0) &&
+                  W.size(1) == act.size(1) && W.size(2) == dOut.size(1),
+              "expected act [A,K], W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  TORCH_CHECK(act_grad.is_contiguous() && act_grad.sizes() == act.sizes() &&
+                  act_grad.scalar_type() == W.scalar_type(),
+              "expected act_grad [A,K] contiguous, in the weights' dtype");
+  check_device(act_grad, "act_grad");
+  const int64_t A = act.size(0), K = act.size(1), N = dOut.size(1);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(act.get_device());
+  Tensor dW = at::empty({E, K, N}, act.options());
+  Tensor dH = at::empty({A, K}, act.options());
+  const int dt = dtype_code(act);
+  Tensor ws = workspace(act, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dw_dx_gelu(dt, act.data_ptr(), W.data_ptr(),
+                                          offsets.data_ptr<int32_t>(), dOut.data_ptr(),
+                                          act_grad.data_ptr(), E, A, K, N, dW.data_ptr(),
+                                          dH.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(act)),
+               "bwd_grouped_gemm_dW_dX_gelu");
+  return {dW, dH};
+}
+
 // Checks a [rows, cols] activation that travels with W's dtype and device.
 void check_act(const Tensor& t, int64_t rows, int64_t cols, const Tensor& like, const char* name) {
   TORCH_CHECK(t.is_contiguous() && t.dim() == 2 && t.size(0) == rows && t.size(1) == cols &&
@@ -620,6 +674,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("combine_backward_inv", &combine_backward_inv, "Combine backward driven by the inverse map");
   m.def("pack_backward_inv", &pack_backward_inv, "Pack backward driven by the inverse map");
   m.def("route_topk", &route_topk, "Fused softmax / top-k / renorm router gate -> (gates, topk)");
+  m.def("bwd_grouped_gemm_dW_dX", &bwd_grouped_gemm_dW_dX,
+        "dW and dX of one projection in one call (a dW with few tiles runs beside the dX)");
+  m.def("bwd_grouped_gemm_dW_dX_gelu", &bwd_grouped_gemm_dW_dX_gelu,
+        "dW of the down projection and the GELU-backward dX in one call");
   m.def("route_topk_count", &route_topk_count,
         "Router gate fused with the per-block expert count -> (gates, topk, dispatch workspace)");
   m.def("dispatch_tokens_counted", &dispatch_tokens_counted,

@@ -127,9 +127,12 @@ class GroupedGEMM_FN(torch.autograd.Function):
         X, expert_offset, weight = ctx.saved_tensors
         out_grad = out_grad.contiguous()
         dX = dW = None
-        if ctx.needs_input_grad[0]:
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
+            # one call: the dW may run beside the dX (same values as the two calls)
+            dW, dX = ext.bwd_grouped_gemm_dW_dX(X, weight, expert_offset, out_grad)
+        elif ctx.needs_input_grad[0]:
             dX = ext.bwd_grouped_gemm_dX_kernel(weight, expert_offset, out_grad)
-        if ctx.needs_input_grad[2]:
+        elif ctx.needs_input_grad[2]:
             dW = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, out_grad)
         return dX, None, dW
 
@@ -161,14 +164,21 @@ class GroupedGeluFFN_FN(torch.autograd.Function):
         X, expert_offset, W_up, W_down, a, g = ctx.saved_tensors
         dy = dy.contiguous()
         dX = dW_up = dW_down = None
-        if ctx.needs_input_grad[3]:
+        need_dH = ctx.needs_input_grad[0] or ctx.needs_input_grad[2]
+        # Each projection's dW and dX in one call: a dW with few 256x256
+        # tiles runs beside its dX in one kernel launch (same values).
+        if ctx.needs_input_grad[3] and need_dH:
+            dW_down, dH = ext.bwd_grouped_gemm_dW_dX_gelu(a, W_down, expert_offset, dy, g)
+        elif ctx.needs_input_grad[3]:
             dW_down = ext.bwd_grouped_gemm_dW_kernel(a, expert_offset, dy)
-        if ctx.needs_input_grad[0] or ctx.needs_input_grad[2]:
+        elif need_dH:
             dH = ext.bwd_grouped_gemm_dX_gelu(W_down, expert_offset, dy, g)
-            if ctx.needs_input_grad[0]:
-                dX = ext.bwd_grouped_gemm_dX_kernel(W_up, expert_offset, dH)
-            if ctx.needs_input_grad[2]:
-                dW_up = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dH)
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
+            dW_up, dX = ext.bwd_grouped_gemm_dW_dX(X, W_up, expert_offset, dH)
+        elif ctx.needs_input_grad[0]:
+            dX = ext.bwd_grouped_gemm_dX_kernel(W_up, expert_offset, dH)
+        elif ctx.needs_input_grad[2]:
+            dW_up = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dH)
         return dX, None, dW_up, dW_down
 
 

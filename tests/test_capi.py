@@ -89,6 +89,10 @@ def test_workspace_sizes_are_sane():
         ("nt_route_topk_count", (None, 8, 4, 2, None, None, None, 24, None, None),
          capi.NT_ERR_INVALID_ARG),  # block size not a power of two
         ("nt_route_topk", (None, 8, 1025, 2, None, None, None, None), capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_grouped_gemm_dw_dx", (99, None, None, None, None, 8, 16, 8, 8, None, None, None, 0,
+                                   None), capi.NT_ERR_DTYPE),
+        ("nt_grouped_gemm_dw_dx_gelu", (capi.NT_BF16, None, None, None, None, None, 8, 16, 8, 8,
+                                        None, None, None, 0, None), capi.NT_ERR_INVALID_ARG),
         ("nt_route_topk_backward", (None, None, None, 8, 1025, 2, None, None),
          capi.NT_ERR_TOO_MANY_EXPERTS),
         ("nt_route_topk_backward", (None, None, None, 8, 64, 33, None, None),

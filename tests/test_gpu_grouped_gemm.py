@@ -213,3 +213,40 @@ def test_split_duty_tiles_ragged(ext, dtype, K, N):
     # deterministic, and rows past the experts' end untouched by neighbours
     again = ext.grouped_gemm_kernel(Xg, og, Wg)
     assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("counts,K,N", [([7680] * 8, 2048, 512), ([7680] * 8, 512, 2048),
+                                        ([20000, 0, 3, 9000, 5000], 1024, 256),
+                                        ([5, 0, 17], 64, 128)])
+def test_paired_dw_dx_matches_separate_calls(ext, dtype, counts, K, N):
+    """bwd_grouped_gemm_dW_dX[_gelu]: the dW runs beside the dX on a second
+    stream when it has few 256x256 tiles (the first three cases; the third
+    also splits its head expert's reduction), else after it. Outputs equal
+    the separate calls bit for bit, and work queued next on the current
+    stream sees them complete."""
+    g = torch.Generator().manual_seed(K + N + len(counts))
+    A, E = sum(counts), len(counts)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    dev = "cuda"
+    X = torch.randn(A, K, generator=g).to(dtype).to(dev)
+    W = (torch.randn(E, K, N, generator=g) / K ** 0.5).to(dtype).to(dev)
+    dOut = torch.randn(A, N, generator=g).to(dtype).to(dev)
+    act_grad = torch.rand(A, K, generator=g).to(dtype).to(dev)
+    og = offsets.to(dev)
+    dW_ref = ext.bwd_grouped_gemm_dW_kernel(X, og, dOut)
+    dX_ref = ext.bwd_grouped_gemm_dX_kernel(W, og, dOut)
+    dH_ref = ext.bwd_grouped_gemm_dX_gelu(W, og, dOut, act_grad)
+    for _ in range(2):  # the second call reuses the side stream and its events
+        dW, dX = ext.bwd_grouped_gemm_dW_dX(X, W, og, dOut)
+        same = torch.equal(dW.view(torch.int16), dW_ref.view(torch.int16)) and \
+            torch.equal(dX.view(torch.int16), dX_ref.view(torch.int16))
+        assert same
+        dW2, dH = ext.bwd_grouped_gemm_dW_dX_gelu(X, W, og, dOut, act_grad)
+        assert torch.equal(dW2.view(torch.int16), dW_ref.view(torch.int16))
+        assert torch.equal(dH.view(torch.int16), dH_ref.view(torch.int16))
+    if A <= 4096:  # the separate calls themselves against the oracle
+        check(dW_ref, O.grouped_gemm_dw(X.cpu(), offsets, dOut.cpu()), dtype,
+              scale=max(counts) ** 0.5)
+        check(dX_ref, O.grouped_gemm_dx(W.cpu(), offsets, dOut.cpu()), dtype)
