@@ -357,12 +357,17 @@ def main():
     prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
     if prof.exists():
         fams_t = json.loads(prof.read_text()).get("families", {})
-        # GEMM launches of one step: up (fused GELU), down, down dX (fused
-        # GELU backward), up dX, and two dW; traffic per launch averaged over them.
-        per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_dx_gelu": 1, "gemm_dx": 1,
-                    "gemm_dw": 2}
+        # GEMM launches of one step: up (fused GELU), down, and the backward's
+        # down dX (fused GELU backward), up dX and two dW, either as paired
+        # launches (dW + dX in one kernel, two GEMMs each) or one by one;
+        # traffic per GEMM averaged over the six.
+        per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_pair_dw_dx_gelu": 1,
+                    "gemm_pair_dw_dx": 1}
+        if not all(f in fams_t for f in per_step):
+            per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_dx_gelu": 1, "gemm_dx": 1,
+                        "gemm_dw": 2}
         if all(f in fams_t for f in per_step):
-            n = sum(per_step.values())
+            n = 6
             roofline["traffic"] = round(sum(fams_t[f]["bytes"] * c for f, c in per_step.items()) / n)
             roofline["traffic_algorithmic"] = round(
                 sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
