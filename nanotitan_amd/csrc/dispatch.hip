@@ -109,6 +109,8 @@ __device__ __forceinline__ void copy_row_to_slots(const V* __restrict__ src, V* 
   }
 }
 
+constexpr int kRowBatch = 8;  // rows in flight per wave in the short-row copy
+
 // Rank, place and copy. base_mode 0: base[e] comes from `base` (cursor copy);
 // base_mode 1: base[e] = exclusive scan of counts (offsets), written to
 // `offsets` by workgroup 0.
@@ -198,10 +200,38 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
   }
 
   // Rows: each wave copies whole token rows, read once, written k times.
-  if (nv > 0) {
-    for (int t = wave; t < ntok; t += kDispatchWaves) {
-      copy_row_to_slots<V>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);
+  if (nv <= 0) return;
+  if constexpr (sizeof(V) == 16) {
+    if (nv <= kWave) {
+      // One vector per lane per row: load kRowBatch rows before storing any,
+      // so a wave waits for memory once per batch rather than once per row.
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4* src = reinterpret_cast<const u32x4*>(X);
+      u32x4* dst = reinterpret_cast<u32x4*>(packed_X);
+      const bool on = lane < nv;
+      for (int t = wave; t < ntok; t += kRowBatch * kDispatchWaves) {
+        u32x4 v[kRowBatch];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          const int tt = t + u * kDispatchWaves;
+          if (on && tt < ntok) v[u] = src[(tok0 + tt) * nv + lane];
+        }
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          const int tt = t + u * kDispatchWaves;
+          if (on && tt < ntok) {
+            for (int j = 0; j < k; ++j) {
+              const int32_t p = s_pos[tt * k + j];
+              if (p >= 0) dst[(int64_t)p * nv + lane] = v[u];
+            }
+          }
+        }
+      }
+      return;
     }
+  }
+  for (int t = wave; t < ntok; t += kDispatchWaves) {
+    copy_row_to_slots<V>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);
   }
 }
 
