@@ -314,6 +314,23 @@ int nt_grouped_gemm_dw_dx_gelu(int dtype, const void* act, const void* W, const 
                                int64_t K, int64_t N, void* dW, void* dH, void* ws,
                                size_t ws_bytes, hipStream_t stream);
 
+/* The same pairing for the SwiGLU FFN's output projection: dW = hidden^T
+ * dOut (nt_grouped_gemm_dw) and (dgate, dvalue) from dhidden = dOut W^T
+ * (nt_grouped_gemm_dx_swiglu). hidden, gate, value, dgate, dvalue [A,K]. */
+int nt_grouped_gemm_dw_dx_swiglu(int dtype, const void* hidden, const void* W,
+                                 const int32_t* offsets, const void* dOut, const void* gate,
+                                 const void* value, int32_t E, int64_t A, int64_t K, int64_t N,
+                                 void* dW, void* dgate, void* dvalue, void* ws, size_t ws_bytes,
+                                 hipStream_t stream);
+
+/* And for its input projections: dW1 = X^T dOut1 (nt_grouped_gemm_dw, the
+ * gate weights' gradient) and dX = dOut1 W1^T + dOut2 W2^T
+ * (nt_grouped_gemm_dx2). X, dX [A,K]; W1, W2 [E,K,N]; dOut1, dOut2 [A,N]. */
+int nt_grouped_gemm_dw_dx2(int dtype, const void* X, const void* W1, const void* W2,
+                           const int32_t* offsets, const void* dOut1, const void* dOut2,
+                           int32_t E, int64_t A, int64_t K, int64_t N, void* dW1, void* dX,
+                           void* ws, size_t ws_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,6 +124,16 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         [c_int, _P, _P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, _P, _P, _P, c_size_t,
          _P],
     ),
+    "nt_grouped_gemm_dw_dx_swiglu": (
+        c_int,
+        [c_int, _P, _P, _P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, _P, _P, _P, _P,
+         c_size_t, _P],
+    ),
+    "nt_grouped_gemm_dw_dx2": (
+        c_int,
+        [c_int, _P, _P, _P, _P, _P, _P, c_int32, c_int64, c_int64, c_int64, _P, _P, _P,
+         c_size_t, _P],
+    ),
 }
 
 

@@ -1931,8 +1931,9 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(kWave), 0, stream, dyn, 8);
   plan_tiles<kDw>(gw, N, 256, 256);
   plan_tiles<kDx>(gx, K, 256, 256);
-  constexpr bool kPlain = EPIX == kEpiPlain;
-  const bool splitx = kPlain && N >= kSplitMinRed;
+  // split duties for the dX as launch_mfma_auto would choose them
+  constexpr bool kPlain = EPIX == kEpiPlain || EPIX == kEpiDualK;
+  const bool splitx = kPlain && (EPIX == kEpiDualK ? 2 * N : N) >= kSplitMinRed;
   const dim3 grid((unsigned)cus);
   const dim3 block(8 * kWave);
   const int32_t nw32 = (int32_t)nw;
@@ -2070,6 +2071,47 @@ int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t
   const uintptr_t al = reinterpret_cast<uintptr_t>(W2) | reinterpret_cast<uintptr_t>(dOut2);
   const bool mfma = mfma_ok(dtype, K, N, dOut1, W1, dX) && al % 16 == 0 && N % 64 == 0;
   return launch_mode<kDx, kEpiDualK>(dtype, g, K, mfma, stream);
+}
+
+int nt_grouped_gemm_dw_dx_swiglu(int dtype, const void* hidden, const void* W,
+                                 const int32_t* offsets, const void* dOut, const void* gate,
+                                 const void* value, int32_t E, int64_t A, int64_t K, int64_t N,
+                                 void* dW, void* dgate, void* dvalue, void* ws, size_t ws_bytes,
+                                 hipStream_t stream) {
+  int st = check_gemm(dtype, E, A, K, N, hidden, dOut, offsets, dW);
+  if (st != NT_OK) return st;
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate);
+  if (st != NT_OK) return st;
+  if (A > 0 && K > 0 && (dvalue == nullptr || gate == nullptr || value == nullptr))
+    return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0)
+    return dw_impl(dtype, hidden, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  GemmArgs gx{dOut, W, offsets, E, A, K, N, dgate, 0, 0, 0, dvalue, gate, 0, nullptr,
+              nullptr, nullptr, nullptr, value};
+  const uintptr_t al = reinterpret_cast<uintptr_t>(dvalue) | reinterpret_cast<uintptr_t>(gate) |
+                       reinterpret_cast<uintptr_t>(value);
+  const bool dx_mfma = mfma_ok(dtype, K, N, dOut, W, dgate) && al % 16 == 0;
+  return pair_dw_dx<kEpiSwiGLUGrad>(dtype, hidden, offsets, dOut, E, A, K, N, dW, ws, ws_bytes,
+                                    gx, dx_mfma, stream);
+}
+
+int nt_grouped_gemm_dw_dx2(int dtype, const void* X, const void* W1, const void* W2,
+                           const int32_t* offsets, const void* dOut1, const void* dOut2,
+                           int32_t E, int64_t A, int64_t K, int64_t N, void* dW1, void* dX,
+                           void* ws, size_t ws_bytes, hipStream_t stream) {
+  int st = check_gemm(dtype, E, A, K, N, X, dOut1, offsets, dW1);
+  if (st != NT_OK) return st;
+  st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX);
+  if (st != NT_OK) return st;
+  if (A > 0 && N > 0 && K > 0 && (W2 == nullptr || dOut2 == nullptr)) return NT_ERR_INVALID_ARG;
+  if (A == 0 || K == 0)
+    return dw_impl(dtype, X, offsets, dOut1, E, A, K, N, dW1, ws, ws_bytes, stream);
+  GemmArgs gx{dOut1, W1, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr,
+              dOut2, W2, nullptr, nullptr};
+  const uintptr_t al = reinterpret_cast<uintptr_t>(W2) | reinterpret_cast<uintptr_t>(dOut2);
+  const bool dx_mfma = mfma_ok(dtype, K, N, dOut1, W1, dX) && al % 16 == 0 && N % 64 == 0;
+  return pair_dw_dx<kEpiDualK>(dtype, X, offsets, dOut1, E, A, K, N, dW1, ws, ws_bytes, gx,
+                               dx_mfma, stream);
 }
 
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,

@@ -381,6 +381,69 @@ std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX_gelu(Tensor act, Tensor W, Ten
   return {dW, dH};
 }
 
+// bwd_grouped_gemm_dW_dX_swiglu(hidden, W_out, expert_offset, dOut, gate, value)
+// -> (dW_out, dgate, dvalue): bwd_grouped_gemm_dW_kernel(hidden, ., dOut) and
+// bwd_grouped_gemm_dX_swiglu(W_out, ., dOut, gate, value) in one call.
+std::tuple<Tensor, Tensor, Tensor> bwd_grouped_gemm_dW_dX_swiglu(Tensor hidden, Tensor W,
+                                                                 Tensor offsets, Tensor dOut,
+                                                                 Tensor gate, Tensor value) {
+  check_gemm_inputs(hidden, offsets, dOut);
+  check_gemm_inputs(dOut, offsets, W);
+  TORCH_CHECK(hidden.dim() == 2 && W.dim() == 3 && dOut.dim() == 2 &&
+                  dOut.size(0) == hidden.size(0) && W.size(1) == hidden.size(1) &&
+                  W.size(2) == dOut.size(1),
+              "expected hidden [A,K], W [E,K,N] and dOut [A,N]");
+  TORCH_CHECK(offsets.numel() == W.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  for (const Tensor* t : {&gate, &value}) {
+    TORCH_CHECK(t->is_contiguous() && t->sizes() == hidden.sizes() &&
+                    t->scalar_type() == W.scalar_type(),
+                "expected gate and value [A,K] contiguous, in the weights' dtype");
+    check_device(*t, "gate/value");
+  }
+  const int64_t A = hidden.size(0), K = hidden.size(1), N = dOut.size(1);
+  const int32_t E = (int32_t)W.size(0);
+  c10::hip::HIPGuard guard(hidden.get_device());
+  Tensor dW = at::empty({E, K, N}, hidden.options());
+  Tensor dgate = at::empty({A, K}, hidden.options());
+  Tensor dvalue = at::empty({A, K}, hidden.options());
+  const int dt = dtype_code(hidden);
+  Tensor ws = workspace(hidden, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dw_dx_swiglu(dt, hidden.data_ptr(), W.data_ptr(),
+                                            offsets.data_ptr<int32_t>(), dOut.data_ptr(),
+                                            gate.data_ptr(), value.data_ptr(), E, A, K, N,
+                                            dW.data_ptr(), dgate.data_ptr(), dvalue.data_ptr(),
+                                            ws.data_ptr(), ws.numel(), stream_of(hidden)),
+               "bwd_grouped_gemm_dW_dX_swiglu");
+  return {dW, dgate, dvalue};
+}
+
+// bwd_grouped_gemm_dW_dX2(X, W1, W2, expert_offset, dOut1, dOut2) -> (dW1, dX):
+// bwd_grouped_gemm_dW_kernel(X, ., dOut1) and bwd_grouped_gemm_dX2 in one call.
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX2(Tensor X, Tensor W1, Tensor W2,
+                                                   Tensor offsets, Tensor dOut1, Tensor dOut2) {
+  check_gemm_inputs(X, offsets, dOut1);
+  check_gemm_inputs(dOut1, offsets, W1);
+  check_gemm_inputs(dOut2, offsets, W2);
+  TORCH_CHECK(X.dim() == 2 && W1.dim() == 3 && W2.sizes() == W1.sizes() && dOut1.dim() == 2 &&
+                  dOut2.sizes() == dOut1.sizes() && dOut1.size(0) == X.size(0) &&
+                  W1.size(1) == X.size(1) && W1.size(2) == dOut1.size(1),
+              "expected X [A,K], W1, W2 [E,K,N] and dOut1, dOut2 [A,N]");
+  TORCH_CHECK(offsets.numel() == W1.size(0) + 1, "expert_offset must hold num_experts + 1 entries");
+  const int64_t A = X.size(0), K = X.size(1), N = dOut1.size(1);
+  const int32_t E = (int32_t)W1.size(0);
+  c10::hip::HIPGuard guard(X.get_device());
+  Tensor dW1 = at::empty({E, K, N}, X.options());
+  Tensor dX = at::empty({A, K}, X.options());
+  const int dt = dtype_code(X);
+  Tensor ws = workspace(X, nt_grouped_gemm_workspace_bytes(dt, E, A, K, N));
+  check_status(nt_grouped_gemm_dw_dx2(dt, X.data_ptr(), W1.data_ptr(), W2.data_ptr(),
+                                      offsets.data_ptr<int32_t>(), dOut1.data_ptr(),
+                                      dOut2.data_ptr(), E, A, K, N, dW1.data_ptr(), dX.data_ptr(),
+                                      ws.data_ptr(), ws.numel(), stream_of(X)),
+               "bwd_grouped_gemm_dW_dX2");
+  return {dW1, dX};
+}
+
 // Checks a [rows, cols] activation that travels with W's dtype and device.
 void check_act(const Tensor& t, int64_t rows, int64_t cols, const Tensor& like, const char* name) {
   TORCH_CHECK(t.is_contiguous() && t.dim() == 2 && t.size(0) == rows && t.size(1) == cols &&
@@ -678,6 +741,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "dW and dX of one projection in one call (a dW with few tiles runs beside the dX)");
   m.def("bwd_grouped_gemm_dW_dX_gelu", &bwd_grouped_gemm_dW_dX_gelu,
         "dW of the down projection and the GELU-backward dX in one call");
+  m.def("bwd_grouped_gemm_dW_dX_swiglu", &bwd_grouped_gemm_dW_dX_swiglu,
+        "dW of the SwiGLU output projection and the SwiGLU-backward dX in one call");
+  m.def("bwd_grouped_gemm_dW_dX2", &bwd_grouped_gemm_dW_dX2,
+        "dW of the gate projection and the two-part dX in one call");
   m.def("route_topk_count", &route_topk_count,
         "Router gate fused with the per-block expert count -> (gates, topk, dispatch workspace)");
   m.def("dispatch_tokens_counted", &dispatch_tokens_counted,

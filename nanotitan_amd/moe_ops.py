@@ -216,16 +216,22 @@ class SwiGLUFFN_FN(torch.autograd.Function):
         X, expert_offset, W_gate, W_val, W_out, h, g, v = ctx.saved_tensors
         dy = dy.contiguous()
         dX = dW_gate = dW_val = dW_out = None
-        if ctx.needs_input_grad[4]:
+        need_d = any(ctx.needs_input_grad[i] for i in (0, 2, 3))
+        # Paired calls (a dW with few tiles runs beside its dX in one launch).
+        if ctx.needs_input_grad[4] and need_d:
+            dW_out, dg, dv = ext.bwd_grouped_gemm_dW_dX_swiglu(h, W_out, expert_offset, dy, g, v)
+        elif ctx.needs_input_grad[4]:
             dW_out = ext.bwd_grouped_gemm_dW_kernel(h, expert_offset, dy)
-        if any(ctx.needs_input_grad[i] for i in (0, 2, 3)):
+        elif need_d:
             dg, dv = ext.bwd_grouped_gemm_dX_swiglu(W_out, expert_offset, dy, g, v)
-            if ctx.needs_input_grad[0]:
-                dX = ext.bwd_grouped_gemm_dX2(W_gate, W_val, expert_offset, dg, dv)
-            if ctx.needs_input_grad[2]:
-                dW_gate = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dg)
-            if ctx.needs_input_grad[3]:
-                dW_val = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dv)
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
+            dW_gate, dX = ext.bwd_grouped_gemm_dW_dX2(X, W_gate, W_val, expert_offset, dg, dv)
+        elif ctx.needs_input_grad[0]:
+            dX = ext.bwd_grouped_gemm_dX2(W_gate, W_val, expert_offset, dg, dv)
+        elif ctx.needs_input_grad[2]:
+            dW_gate = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dg)
+        if ctx.needs_input_grad[3]:
+            dW_val = ext.bwd_grouped_gemm_dW_kernel(X, expert_offset, dv)
         return dX, None, dW_gate, dW_val, dW_out
 
 

@@ -250,3 +250,39 @@ def test_paired_dw_dx_matches_separate_calls(ext, dtype, counts, K, N):
         check(dW_ref, O.grouped_gemm_dw(X.cpu(), offsets, dOut.cpu()), dtype,
               scale=max(counts) ** 0.5)
         check(dX_ref, O.grouped_gemm_dx(W.cpu(), offsets, dOut.cpu()), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("counts,K,N", [([7680] * 8, 2048, 512), ([7680] * 8, 512, 2048),
+                                        ([9000, 0, 1, 4000], 256, 1024), ([5, 0, 17], 64, 128)])
+def test_paired_swiglu_backward_matches_separate_calls(ext, dtype, counts, K, N):
+    """bwd_grouped_gemm_dW_dX_swiglu (dW of the output projection beside the
+    SwiGLU-backward dX) and bwd_grouped_gemm_dW_dX2 (dW of the gate
+    projection beside the two-part dX) equal the separate calls bit for bit."""
+    g = torch.Generator().manual_seed(K * 3 + N + len(counts))
+    A, E = sum(counts), len(counts)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    og = offsets.cuda()
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dtype).cuda()
+
+    bits = lambda t: t.view(torch.int16)  # noqa: E731
+    # output projection: hidden/gate/value [A,K], W_out [E,K,N], dy [A,N]
+    h, gate, value = rnd(A, K), rnd(A, K), rnd(A, K)
+    W_out, dy = rnd(E, K, N, scale=K ** -0.5), rnd(A, N)
+    dW_ref = ext.bwd_grouped_gemm_dW_kernel(h, og, dy)
+    dg_ref, dv_ref = ext.bwd_grouped_gemm_dX_swiglu(W_out, og, dy, gate, value)
+    for _ in range(2):
+        dW, dg, dv = ext.bwd_grouped_gemm_dW_dX_swiglu(h, W_out, og, dy, gate, value)
+        assert torch.equal(bits(dW), bits(dW_ref))
+        assert torch.equal(bits(dg), bits(dg_ref)) and torch.equal(bits(dv), bits(dv_ref))
+    # input projections: X [A,K], W_gate / W_val [E,K,N], dgate / dvalue [A,N]
+    X, W1, W2 = rnd(A, K), rnd(E, K, N, scale=K ** -0.5), rnd(E, K, N, scale=K ** -0.5)
+    d1, d2 = rnd(A, N), rnd(A, N)
+    dW1_ref = ext.bwd_grouped_gemm_dW_kernel(X, og, d1)
+    dX_ref = ext.bwd_grouped_gemm_dX2(W1, W2, og, d1, d2)
+    for _ in range(2):
+        dW1, dX = ext.bwd_grouped_gemm_dW_dX2(X, W1, W2, og, d1, d2)
+        assert torch.equal(bits(dW1), bits(dW1_ref)) and torch.equal(bits(dX), bits(dX_ref))
