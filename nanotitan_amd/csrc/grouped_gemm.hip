@@ -1814,14 +1814,21 @@ int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t 
   return launch_gelu_elementwise<true>(dtype, g.out, const_cast<void*>(g.aux), n, s);
 }
 
+// Argument check of one grouped GEMM of `mode`: fwd out[A,N] = a[A,K] b[E,K,N];
+// dX out[A,K] = a[A,N] b[E,K,N]^T; dW out[E,K,N] = a[A,K]^T b[A,N]. Pointers
+// of empty tensors may be null.
 int check_gemm(int dtype, int32_t E, int64_t A, int64_t K, int64_t N, const void* a,
-               const void* b, const int32_t* offsets, const void* out) {
+               const void* b, const int32_t* offsets, const void* out, int mode = kFwd) {
   if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
   if (E < 1 || A < 0 || K < 0 || N < 0) return NT_ERR_INVALID_ARG;
   if (E > NT_MAX_EXPERTS) return NT_ERR_TOO_MANY_EXPERTS;
   if (offsets == nullptr) return NT_ERR_INVALID_ARG;
-  if ((A > 0 && K > 0 && a == nullptr) || (K > 0 && N > 0 && b == nullptr)) return NT_ERR_INVALID_ARG;
-  if (out == nullptr && ((A > 0 && (K > 0 || N > 0)) || (K > 0 && N > 0))) return NT_ERR_INVALID_ARG;
+  const int64_t a_cols = mode == kDx ? N : K;
+  const int64_t b_elems = mode == kDw ? A * N : K * N;
+  const int64_t out_elems = mode == kDw ? K * N : A * (mode == kDx ? K : N);
+  if ((A * a_cols > 0 && a == nullptr) || (b_elems > 0 && b == nullptr) ||
+      (out_elems > 0 && out == nullptr))
+    return NT_ERR_INVALID_ARG;
   if (A > INT32_MAX) return NT_ERR_TOO_LARGE;
   // Tile operand and output offsets are 32-bit byte offsets: 256 rows of
   // the widest operand row must stay below 2 GiB.
@@ -2002,7 +2009,7 @@ int nt_grouped_gemm_dx(int dtype, const void* W, const int32_t* offsets, const v
                        size_t ws_bytes, hipStream_t stream) {
   (void)ws;
   (void)ws_bytes;
-  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX, kDx);
   if (st != NT_OK) return st;
   return dx_impl<kEpiPlain>(dtype, W, offsets, dOut, nullptr, E, A, K, N, dX, stream);
 }
@@ -2012,7 +2019,7 @@ int nt_grouped_gemm_dx_gelu(int dtype, const void* W, const int32_t* offsets, co
                             void* dH, void* ws, size_t ws_bytes, hipStream_t stream) {
   (void)ws;
   (void)ws_bytes;
-  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH);
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH, kDx);
   if (st != NT_OK) return st;
   if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
   return dx_impl<kEpiGeluGrad>(dtype, W, offsets, dOut, act_grad, E, A, K, N, dH, stream);
@@ -2043,7 +2050,7 @@ int nt_grouped_gemm_dx_swiglu(int dtype, const void* W, const int32_t* offsets, 
                               size_t ws_bytes, hipStream_t stream) {
   (void)ws;
   (void)ws_bytes;
-  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate);
+  int st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate, kDx);
   if (st != NT_OK) return st;
   if (A > 0 && K > 0 && (dvalue == nullptr || gate == nullptr || value == nullptr))
     return NT_ERR_INVALID_ARG;
@@ -2061,7 +2068,7 @@ int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t
                         int64_t N, void* dX, void* ws, size_t ws_bytes, hipStream_t stream) {
   (void)ws;
   (void)ws_bytes;
-  int st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX);
+  int st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX, kDx);
   if (st != NT_OK) return st;
   if (A > 0 && N > 0 && K > 0 && (W2 == nullptr || dOut2 == nullptr)) return NT_ERR_INVALID_ARG;
   if (A == 0 || K == 0) return NT_OK;
@@ -2078,14 +2085,13 @@ int nt_grouped_gemm_dw_dx_swiglu(int dtype, const void* hidden, const void* W,
                                  const void* value, int32_t E, int64_t A, int64_t K, int64_t N,
                                  void* dW, void* dgate, void* dvalue, void* ws, size_t ws_bytes,
                                  hipStream_t stream) {
-  int st = check_gemm(dtype, E, A, K, N, hidden, dOut, offsets, dW);
+  int st = check_gemm(dtype, E, A, K, N, hidden, dOut, offsets, dW, kDw);
   if (st != NT_OK) return st;
-  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate);
-  if (st != NT_OK) return st;
-  if (A > 0 && K > 0 && (dvalue == nullptr || gate == nullptr || value == nullptr))
-    return NT_ERR_INVALID_ARG;
   if (A == 0 || K == 0)
     return dw_impl(dtype, hidden, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dgate, kDx);
+  if (st != NT_OK) return st;
+  if (dvalue == nullptr || gate == nullptr || value == nullptr) return NT_ERR_INVALID_ARG;
   GemmArgs gx{dOut, W, offsets, E, A, K, N, dgate, 0, 0, 0, dvalue, gate, 0, nullptr,
               nullptr, nullptr, nullptr, value};
   const uintptr_t al = reinterpret_cast<uintptr_t>(dvalue) | reinterpret_cast<uintptr_t>(gate) |
@@ -2099,13 +2105,13 @@ int nt_grouped_gemm_dw_dx2(int dtype, const void* X, const void* W1, const void*
                            const int32_t* offsets, const void* dOut1, const void* dOut2,
                            int32_t E, int64_t A, int64_t K, int64_t N, void* dW1, void* dX,
                            void* ws, size_t ws_bytes, hipStream_t stream) {
-  int st = check_gemm(dtype, E, A, K, N, X, dOut1, offsets, dW1);
+  int st = check_gemm(dtype, E, A, K, N, X, dOut1, offsets, dW1, kDw);
   if (st != NT_OK) return st;
-  st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX);
-  if (st != NT_OK) return st;
-  if (A > 0 && N > 0 && K > 0 && (W2 == nullptr || dOut2 == nullptr)) return NT_ERR_INVALID_ARG;
   if (A == 0 || K == 0)
     return dw_impl(dtype, X, offsets, dOut1, E, A, K, N, dW1, ws, ws_bytes, stream);
+  st = check_gemm(dtype, E, A, K, N, dOut1, W1, offsets, dX, kDx);
+  if (st != NT_OK) return st;
+  if (N > 0 && (W2 == nullptr || dOut2 == nullptr)) return NT_ERR_INVALID_ARG;
   GemmArgs gx{dOut1, W1, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr,
               dOut2, W2, nullptr, nullptr};
   const uintptr_t al = reinterpret_cast<uintptr_t>(W2) | reinterpret_cast<uintptr_t>(dOut2);
@@ -2117,7 +2123,7 @@ int nt_grouped_gemm_dw_dx2(int dtype, const void* X, const void* W1, const void*
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
-  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
+  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW, kDw);
   if (st != NT_OK) return st;
   return dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
 }
@@ -2125,11 +2131,12 @@ int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const v
 int nt_grouped_gemm_dw_dx(int dtype, const void* X, const void* W, const int32_t* offsets,
                           const void* dOut, int32_t E, int64_t A, int64_t K, int64_t N, void* dW,
                           void* dX, void* ws, size_t ws_bytes, hipStream_t stream) {
-  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW);
+  int st = check_gemm(dtype, E, A, K, N, X, dOut, offsets, dW, kDw);
   if (st != NT_OK) return st;
-  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX);
-  if (st != NT_OK) return st;
+  // No rows (or no dX columns): only the dW (zero for empty experts).
   if (A == 0 || K == 0) return dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dX, kDx);
+  if (st != NT_OK) return st;
   GemmArgs gx{dOut, W, offsets, E, A, K, N, dX, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   return pair_dw_dx<kEpiPlain>(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, gx,
                                mfma_ok(dtype, K, N, dOut, W, dX), stream);
@@ -2139,13 +2146,13 @@ int nt_grouped_gemm_dw_dx_gelu(int dtype, const void* act, const void* W, const 
                                const void* dOut, const void* act_grad, int32_t E, int64_t A,
                                int64_t K, int64_t N, void* dW, void* dH, void* ws,
                                size_t ws_bytes, hipStream_t stream) {
-  int st = check_gemm(dtype, E, A, K, N, act, dOut, offsets, dW);
+  int st = check_gemm(dtype, E, A, K, N, act, dOut, offsets, dW, kDw);
   if (st != NT_OK) return st;
-  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH);
-  if (st != NT_OK) return st;
-  if (act_grad == nullptr && A > 0 && K > 0) return NT_ERR_INVALID_ARG;
   if (A == 0 || K == 0)
     return dw_impl(dtype, act, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
+  st = check_gemm(dtype, E, A, K, N, dOut, W, offsets, dH, kDx);
+  if (st != NT_OK) return st;
+  if (act_grad == nullptr) return NT_ERR_INVALID_ARG;
   GemmArgs gx{dOut, W, offsets, E, A, K, N, dH, 0, 0, 0, nullptr, act_grad, 0, nullptr};
   const bool dx_mfma = mfma_ok(dtype, K, N, dOut, W, dH) &&
                        reinterpret_cast<uintptr_t>(act_grad) % 16 == 0;

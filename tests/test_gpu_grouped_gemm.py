@@ -286,3 +286,28 @@ def test_paired_swiglu_backward_matches_separate_calls(ext, dtype, counts, K, N)
     for _ in range(2):
         dW1, dX = ext.bwd_grouped_gemm_dW_dX2(X, W1, W2, og, d1, d2)
         assert torch.equal(bits(dW1), bits(dW1_ref)) and torch.equal(bits(dX), bits(dX_ref))
+
+
+@pytest.mark.parametrize("dtype,counts,K,N", [
+    (torch.float32, [700, 0, 300], 96, 160),      # generic FMA path: no pairing
+    (torch.bfloat16, [700, 0, 300], 40, 24),      # K, N not multiples of 64 / 8
+    (torch.bfloat16, [0, 0, 0], 64, 128),         # no rows at all
+    (torch.bfloat16, [500] * 20, 256, 256),       # more experts than the pairing limit
+])
+def test_paired_calls_edge_cases(ext, dtype, counts, K, N):
+    """Paired ops fall back to the separate GEMMs where they cannot pair and
+    still match them (and the oracle within tolerance)."""
+    g = torch.Generator().manual_seed(K + N)
+    A, E = sum(counts), len(counts)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    X = torch.randn(A, K, generator=g).to(dtype)
+    W = (torch.randn(E, K, N, generator=g) / K ** 0.5).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    Xg, Wg, og, Gg = X.cuda(), W.cuda(), offsets.cuda(), G.cuda()
+    dW, dX = ext.bwd_grouped_gemm_dW_dX(Xg, Wg, og, Gg)
+    assert torch.equal(dW, ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg))
+    assert torch.equal(dX, ext.bwd_grouped_gemm_dX_kernel(Wg, og, Gg))
+    check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(max(counts), 1) ** 0.5)
+    if A:
+        check(dX, O.grouped_gemm_dx(W, offsets, G), dtype)
