@@ -48,11 +48,11 @@ def _gelu_grad(x):
     return 0.5 * (1 + torch.erf(x / 2 ** 0.5)) + x * torch.exp(-0.5 * x * x) / (2 * torch.pi) ** 0.5
 
 
-def _cuda_weights(c, seed):
+def _cuda_weights(c, seed, n=2):
+    """n = 2: W_up [E,d,f], W_down [E,f,d]; n = 3: W_gate, W_val [E,d,f], W_out [E,f,d]."""
     g = torch.Generator(device="cuda").manual_seed(seed)
-    W_up = (torch.randn(c.E, c.d, c.f, generator=g, device="cuda") * c.w_std).to(c.dtype)
-    W_down = (torch.randn(c.E, c.f, c.d, generator=g, device="cuda") * c.w_std).to(c.dtype)
-    return W_up, W_down
+    shapes = [(c.E, c.d, c.f)] * (n - 1) + [(c.E, c.f, c.d)]
+    return [(torch.randn(*s, generator=g, device="cuda") * c.w_std).to(c.dtype) for s in shapes]
 
 
 def _sample_tokens(idx, logits, E, seed, n=32):
@@ -71,21 +71,26 @@ def _sample_tokens(idx, logits, E, seed, n=32):
     return torch.tensor(sorted(pick), dtype=torch.long)
 
 
-@pytest.mark.parametrize("cfg_id", [1, 2, 3, 4, 5])
-def test_layer_full_size_sampled_tokens(ext, cfg_id):
+@pytest.mark.parametrize("cfg_id,ffn", [(1, "gelu"), (2, "gelu"), (3, "gelu"), (4, "gelu"),
+                                        (5, "gelu"), (2, "swiglu"), (4, "swiglu")])
+def test_layer_full_size_sampled_tokens(ext, cfg_id, ffn):
     """The layer forward + backward at the config's full token count (the
-    benchmark's path: router with fused count, dispatch, fused GELU expert FFN,
-    combine), vs the oracle's torch path on a sample of tokens."""
+    benchmark's path: router with fused count, dispatch, fused expert FFN,
+    combine), vs the oracle's torch path on a sample of tokens. GELU is the
+    configs' FFN; SwiGLU is the reference's ExpertFFN at the configs' widths."""
     from nanotitan_amd.layer import moe_forward_from_logits
-    from nanotitan_amd.moe_ops import grouped_gelu_ffn_fn
+    from nanotitan_amd.moe_ops import grouped_gelu_ffn_fn, swiglu_ffn_fn
 
     d = O.make_inputs(cfg_id, with_weights=False)
     c = d["cfg"]
-    W_up, W_down = _cuda_weights(c, 7000 + cfg_id)
+    names = ["up", "down"] if ffn == "gelu" else ["gate", "val", "out"]
+    W = dict(zip(names, _cuda_weights(c, 7000 + cfg_id, len(names))))
 
     class FFN(torch.nn.Module):
         def forward(self, px, off):
-            return grouped_gelu_ffn_fn(px, W_up, W_down, off)
+            if ffn == "gelu":
+                return grouped_gelu_ffn_fn(px, W["up"], W["down"], off)
+            return swiglu_ffn_fn(px, W["gate"], W["val"], W["out"], off)
 
     x = d["X"].to(c.dtype).cuda().requires_grad_(True)
     logits = d["logits"].cuda().requires_grad_(True)
@@ -100,9 +105,9 @@ def test_layer_full_size_sampled_tokens(ext, cfg_id):
     assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(x.grad).all())
 
     S = _sample_tokens(idx, d["logits"], c.E, seed=cfg_id)
-    weights = {"up": W_up.cpu(), "down": W_down.cpu()}
+    weights = {n: w.cpu() for n, w in W.items()}
     ref_out, ref = O.moe_layer_torch(d["X"][S].to(c.dtype), d["logits"][S], weights, c.k,
-                                     ffn="gelu", dY=d["dY"][S].to(c.dtype))
+                                     ffn=ffn, dY=d["dY"][S].to(c.dtype))
     tol = dict(rtol=1e-4, atol=1e-4) if c.dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
     torch.testing.assert_close(out.detach()[S.cuda()].cpu().float(), ref_out.float(), **tol)
     torch.testing.assert_close(x.grad[S.cuda()].cpu().float(), ref["x"].float(), **tol)
