@@ -89,6 +89,7 @@ class LaunchTimer:
         "bwd_grouped_gemm_dW_dX": "gemm",
         "bwd_grouped_gemm_dW_dX_gelu": "gemm",
         "dispatch_tokens": "dispatch",
+        "dispatch_tokens_counted": "dispatch",
         "combine_inv": "combine_fwd",
         "combine_backward_inv": "combine_bwd",
         "pack_backward_inv": "pack_bwd",
@@ -139,8 +140,9 @@ class LaunchTimer:
         if name in ("bwd_grouped_gemm_dW_dX", "bwd_grouped_gemm_dW_dX_gelu"):
             X, _W, _off, G = args[:4]
             return 2 * 2.0 * X.shape[0] * X.shape[1] * G.shape[1]
-        if name == "dispatch_tokens":  # read X once, write packed rows, ids/gates
-            X, w, topk, _E = args
+        if name in ("dispatch_tokens", "dispatch_tokens_counted"):
+            # read X once, write packed rows, ids/gates
+            X, w, topk = args[:3]
             T, d = X.shape
             A = topk.numel()
             b = X.element_size()

@@ -170,6 +170,23 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
   const int na = ntok * k;
   const int64_t f0 = tok0 * k;
 
+  // Short rows (one 16-byte vector per lane): the wave's first kRowBatch
+  // token rows are loaded before the ranking, so their latency hides behind
+  // it; only the store addresses depend on the ranks.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr bool kVec16 = sizeof(V) == 16;
+  const bool short_rows = kVec16 && nv > 0 && nv <= kWave;
+  const bool on = lane < nv;
+  u32x4 pre[kRowBatch];
+  if (short_rows) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(X);
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      const int tt = wave + u * kDispatchWaves;
+      if (on && tt < ntok) pre[u] = src[(tok0 + tt) * nv + lane];
+    }
+  }
+
   // Stable rank of each assignment among same-expert assignments of the block.
   for (int r = 0; r < na; r += kDispatchThreads) {
     const int i = r + tid;
@@ -201,20 +218,20 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
 
   // Rows: each wave copies whole token rows, read once, written k times.
   if (nv <= 0) return;
-  if constexpr (sizeof(V) == 16) {
-    if (nv <= kWave) {
-      // One vector per lane per row: load kRowBatch rows before storing any,
-      // so a wave waits for memory once per batch rather than once per row.
-      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  if constexpr (kVec16) {
+    if (short_rows) {
+      // One vector per lane per row: kRowBatch rows are loaded before any is
+      // stored, so a wave waits for memory once per batch rather than once
+      // per row. The first batch was loaded before the ranking.
       const u32x4* src = reinterpret_cast<const u32x4*>(X);
       u32x4* dst = reinterpret_cast<u32x4*>(packed_X);
-      const bool on = lane < nv;
       for (int t = wave; t < ntok; t += kRowBatch * kDispatchWaves) {
         u32x4 v[kRowBatch];
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u) {
           const int tt = t + u * kDispatchWaves;
-          if (on && tt < ntok) v[u] = src[(tok0 + tt) * nv + lane];
+          if (t == wave) v[u] = pre[u];
+          else if (on && tt < ntok) v[u] = src[(tok0 + tt) * nv + lane];
         }
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u) {
