@@ -109,7 +109,7 @@ __device__ __forceinline__ void copy_row_to_slots(const V* __restrict__ src, V* 
   }
 }
 
-constexpr int kRowBatch = 8;  // rows in flight per wave in the short-row copy
+constexpr int kRowBatch = 16;  // rows in flight per wave in the short-row copy
 
 // Rank, place and copy. base_mode 0: base[e] comes from `base` (cursor copy);
 // base_mode 1: base[e] = exclusive scan of counts (offsets), written to
