@@ -69,19 +69,19 @@ __device__ void build_m_prefix(const int32_t* __restrict__ offsets, int E, int64
   __syncthreads();
 }
 
-// dW reduction chunks. Expert e's rows are cut into nch(e) = max(1,
-// ceil(M_e / R)) chunks of R rows (an empty expert keeps one empty chunk, so
-// its dW is still written, as zeros). s_pref[e] = chunks of experts < e;
-// s_split[e] = chunks of experts < e that have at least two (those write
-// fp32 partials, one slab per chunk, and a reduce pass sums them in chunk
-// order). R = 0 means one chunk per expert. Ends with a workgroup barrier.
-__device__ __forceinline__ int dw_chunks(int64_t rows, int32_t R) {
-  if (R <= 0) return 1;
-  const int n = (int)ceil_div(rows, R);
-  return n < 1 ? 1 : n;
+// dW reduction chunks. An expert with more than `thr` rows is cut into
+// nch(e) = ceil(M_e / R) chunks of R rows (R <= thr); every other expert is
+// one chunk (an empty expert keeps one empty chunk, so its dW is still
+// written, as zeros). s_pref[e] = chunks of experts < e; s_split[e] = chunks
+// of experts < e that have at least two (those write fp32 partials, one slab
+// per chunk, and a reduce pass sums them in chunk order). R = 0 means one
+// chunk per expert. Ends with a workgroup barrier.
+__device__ __forceinline__ int dw_chunks(int64_t rows, int32_t R, int32_t thr) {
+  if (R <= 0 || rows <= thr) return 1;
+  return (int)ceil_div(rows, R);
 }
 __device__ void build_chunk_prefix(const int32_t* __restrict__ offsets, int E, int64_t A,
-                                   int32_t R, int32_t* s_pref, int32_t* s_split) {
+                                   int32_t R, int32_t thr, int32_t* s_pref, int32_t* s_split) {
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
     int carry = 0, carry_s = 0;
@@ -91,7 +91,7 @@ __device__ void build_chunk_prefix(const int32_t* __restrict__ offsets, int E, i
       if (e < E) {
         int64_t a, b;
         expert_rows(offsets, e, A, a, b);
-        v = dw_chunks(b - a, R);
+        v = dw_chunks(b - a, R, thr);
         vs = v >= 2 ? v : 0;
       }
       const int incl = wave_incl_scan(v);
@@ -400,6 +400,7 @@ struct GemmArgs {
   const void* b2;
   void* out3;
   const void* aux2;
+  int32_t split_thr;  // dW: experts with more rows than this are split (when chunk > 0)
 };
 
 // Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
@@ -485,7 +486,7 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
     c = (int64_t)__builtin_amdgcn_readfirstlane((int)c);
     const int nch = s_pref[e + 1] - s_pref[e];
     int64_t c0 = r0, c1 = r1;
-    if (g.chunk > 0) {
+    if (nch >= 2) {
       c0 = r0 + c * g.chunk;
       c1 = c0 + g.chunk < r1 ? c0 + g.chunk : r1;
     }
@@ -1081,7 +1082,8 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
     build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
     mtiles = s_pref[g.E];
   } else {
-    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, s_pref, s_pref + (NT_MAX_EXPERTS + 1));
+    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, g.split_thr, s_pref,
+                       s_pref + (NT_MAX_EXPERTS + 1));
     mtiles = (int64_t)s_pref[g.E] * g.ntm;
   }
   const int64_t total = mtiles * g.ntn;
@@ -1680,6 +1682,7 @@ int launch_swiglu_elementwise(int dtype, void* io, void* dg, const void* g, cons
 template <typename T>
 __global__ void __launch_bounds__(256)
 dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int32_t R,
+                 int32_t thr,
                  const float* __restrict__ partial, int64_t KN,
                  typename elem<T>::storage* __restrict__ dW) {
   __shared__ int32_t s_info[2];
@@ -1689,7 +1692,7 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
     // prefix (the common case for balanced routing). Uniform per block.
     int64_t a, b;
     expert_rows(offsets, e, A, a, b);
-    if (dw_chunks(b - a, R) < 2) return;
+    if (dw_chunks(b - a, R, thr) < 2) return;
   }
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
@@ -1700,7 +1703,7 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
       if (ee < e) {
         int64_t a, b;
         expert_rows(offsets, ee, A, a, b);
-        v = dw_chunks(b - a, R);
+        v = dw_chunks(b - a, R, thr);
         v = v >= 2 ? v : 0;
       }
       before += wave_sum_int(v);
@@ -1709,7 +1712,7 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
       int64_t a, b;
       expert_rows(offsets, e, A, a, b);
       s_info[0] = before;
-      s_info[1] = dw_chunks(b - a, R);
+      s_info[1] = dw_chunks(b - a, R, thr);
     }
   }
   __syncthreads();
@@ -1735,10 +1738,11 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
   }
 }
 
-// Rows per dW reduction chunk: at least twice the mean expert size and
-// 1024, and large enough that the fp32 partial slabs of the split experts
-// (fewer than 2A/R of them) fit kDwBudget bytes. 0: no expert can split.
-constexpr int64_t kDwBudget = int64_t(64) << 20;
+// Rows per expert chunk used to estimate a dW launch's tile count for its
+// tile-shape choice: at least twice the mean expert size and 1024, and
+// large enough that the fp32 partial slabs (fewer than 2A/R of them) fit
+// kDwBudget bytes. 0: no expert can split.
+constexpr int64_t kDwBudget = int64_t(256) << 20;
 int32_t dw_chunk_rows(int64_t A, int64_t K, int64_t N, int32_t E) {
   const int64_t slab = K * N * 4;
   if (A <= 0 || slab <= 0 || E <= 0) return 0;
@@ -1749,13 +1753,55 @@ int32_t dw_chunk_rows(int64_t A, int64_t K, int64_t N, int32_t E) {
   if (R >= A) return 0;
   return (int32_t)R;
 }
+
+// Split of every dW launch, paired or not (the same split gives the same
+// summation order, so the paired and separate calls agree bit for bit).
+// W = A * (128x128 tiles per expert) / (two workgroups per CU) is a
+// workgroup's share of the reduction rows. An expert with more than
+// thr = 5W/4 rows is cut into chunks of R = W/2 rows (at least 1024, and at
+// least what keeps the slabs within kDwBudget), so no tile is much longer
+// than a share: with skewed routing (C3: the head expert has 8x the mean
+// rows) one whole-expert tile would otherwise outlast everything else.
+// Balanced routing stays unsplit.
+struct DwSplit {
+  int32_t R = 0;    // rows per chunk of a split expert (0: no split)
+  int32_t thr = 0;  // experts with more rows than this are split
+};
+DwSplit dw_split(int64_t A, int64_t K, int64_t N, int32_t E) {
+  DwSplit p;
+  const int64_t slab = K * N * 4;
+  if (A <= 0 || slab <= 0 || E <= 0 || slab >= kDwBudget) return p;
+  const int64_t W = ceil_div(A * ceil_div(K, 128) * ceil_div(N, 128), 2 * device_cus());
+  int64_t R = std::max<int64_t>(ceil_div(W, 2), 1024);
+  R = round_up(std::max<int64_t>(R, ceil_div(2 * A * slab, kDwBudget)), 64);
+  const int64_t thr = std::max<int64_t>(round_up(ceil_div(5 * W, 4), 64), R);
+  if (thr >= A) return p;
+  p.R = (int32_t)R;
+  p.thr = (int32_t)thr;
+  return p;
+}
+// Upper bound on the partial slabs: at most A / (thr + 1) experts are split
+// (more than thr rows each), and their ceil(M_e / R) chunks add up to at
+// most A / R plus one per split expert.
+int64_t dw_slabs(int64_t A, DwSplit p) {
+  if (p.R <= 0) return 0;
+  return A / p.R + A / ((int64_t)p.thr + 1) + 1;
+}
+
+// Tile shape of a dW launch (not paired): 256x256 tiles when the experts'
+// tiles (with dw_chunk_rows chunks) give at least 1.5 per CU, else 128x128
+// tiles, two workgroups per CU (the rule launch_mfma_auto applies).
+bool dw_big_tiles(int64_t A, int64_t K, int64_t N, int32_t E) {
+  const int32_t R0 = dw_chunk_rows(A, K, N, E);
+  const int64_t chunks = R0 > 0 ? E + A / R0 : E;
+  return chunks * ceil_div(K, 256) * ceil_div(N, 256) * 2 >= device_cus() * 3;
+}
+
 // Workspace of the dW entry points: kCtrBytes of tile counters (paired
 // launches), then the fp32 partial slabs of split experts.
 constexpr size_t kCtrBytes = 256;
 size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
-  const int32_t R = dw_chunk_rows(A, K, N, E);
-  if (R == 0) return 0;
-  return (size_t)ceil_div(2 * A, R) * (size_t)(K * N * 4);
+  return (size_t)dw_slabs(A, dw_split(A, K, N, E)) * (size_t)(K * N * 4);
 }
 
 template <int MODE, int EPI>
@@ -1856,15 +1902,15 @@ int dx_impl(int dtype, const void* W, const int32_t* offsets, const void* dOut,
 }
 
 int launch_dw_reduce(int dtype, const int32_t* offsets, int32_t E, int64_t A, int64_t K,
-                     int64_t N, int32_t R, const float* partial, void* dW, hipStream_t stream) {
+                     int64_t N, DwSplit sp, const float* partial, void* dW, hipStream_t stream) {
   const int64_t KN = K * N;
   const dim3 grid((unsigned)std::min<int64_t>(ceil_div(KN, 256 * 8), 64), (unsigned)E);
   if (dtype == NT_BF16)
-    hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, R,
-                       partial, KN, static_cast<uint16_t*>(dW));
+    hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, sp.R,
+                       sp.thr, partial, KN, static_cast<uint16_t*>(dW));
   else
-    hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, R,
-                       partial, KN, static_cast<uint16_t*>(dW));
+    hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, sp.R,
+                       sp.thr, partial, KN, static_cast<uint16_t*>(dW));
   return launch_status();
 }
 
@@ -1874,19 +1920,23 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
   if (K == 0 || N == 0) return NT_OK;
   GemmArgs g{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   const bool mfma = mfma_ok(dtype, K, N, X, dOut, dW);
+  if (!mfma) return launch_mode<kDw, kEpiPlain>(dtype, g, N, false, stream);
   // Split long reductions (skewed experts) when the caller's workspace holds
   // the partial slabs; without it every expert is one chunk.
-  const int32_t R = mfma ? dw_chunk_rows(A, K, N, E) : 0;
-  const bool split = R > 0 && ws != nullptr && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E) &&
+  const DwSplit sp = dw_split(A, K, N, E);
+  const bool split = sp.R > 0 && ws != nullptr && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E) &&
                      reinterpret_cast<uintptr_t>(ws) % 16 == 0;
   float* partial = split ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCtrBytes) : nullptr;
   if (split) {
-    g.chunk = R;
+    g.chunk = sp.R;
+    g.split_thr = sp.thr;
     g.partial = partial;
   }
-  int st = launch_mode<kDw, kEpiPlain>(dtype, g, N, mfma, stream);
+  const int st = dw_big_tiles(A, K, N, E)
+                     ? launch_mfma<kDw, kEpiPlain, 256, 256, 2, 4, 64, 2>(dtype, g, N, stream)
+                     : launch_mfma<kDw, kEpiPlain, 128, 128, 2, 2, 64, 2>(dtype, g, N, stream);
   if (st != NT_OK || !split) return st;
-  return launch_dw_reduce(dtype, offsets, E, A, K, N, R, partial, dW, stream);
+  return launch_dw_reduce(dtype, offsets, E, A, K, N, sp, partial, dW, stream);
 }
 
 // dW = X^T dOut and a dX-type GEMM (gx, epilogue EPIX) over the same
@@ -1907,9 +1957,9 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
                GemmArgs gx, bool dx_mfma, hipStream_t stream) {
   const int64_t cus = device_cus();
   const bool mfma_dw = mfma_ok(dtype, K, N, X, dOut, dW);
-  const int32_t R = mfma_dw ? dw_chunk_rows(A, K, N, E) : 0;
+  const DwSplit sp = mfma_dw ? dw_split(A, K, N, E) : DwSplit();
   const bool aligned = ws != nullptr && reinterpret_cast<uintptr_t>(ws) % 16 == 0;
-  const bool split = R > 0 && aligned && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E);
+  const bool split = sp.R > 0 && aligned && ws_bytes >= kCtrBytes + dw_ws_bytes(A, K, N, E);
   // Workgroups for the dW: one per tile of the experts' full reductions. A
   // skewed expert split into chunks adds tiles that the same workgroups
   // walk (the persistent loop counts the tiles on the device); sizing for
@@ -1931,7 +1981,8 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   GemmArgs gw{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   float* partial = split ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCtrBytes) : nullptr;
   if (split) {
-    gw.chunk = R;
+    gw.chunk = sp.R;
+    gw.split_thr = sp.thr;
     gw.partial = partial;
   }
   int32_t* dyn = static_cast<int32_t*>(ws);
@@ -1961,7 +2012,7 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   }
   int st = launch_status();
   if (st != NT_OK || !split) return st;
-  return launch_dw_reduce(dtype, offsets, E, A, K, N, R, partial, dW, stream);
+  return launch_dw_reduce(dtype, offsets, E, A, K, N, sp, partial, dW, stream);
 }
 
 }  // namespace

@@ -179,6 +179,54 @@ def test_dw_split_reduction_for_skewed_experts(ext, dtype, counts):
             assert not a[e].any()
 
 
+def _ceil(a, b):
+    return -(-a // b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dw_skewed_split_threshold(ext, dtype):
+    """C3 widths (K=512, N=256, 64 experts), 128x128 dW tiles. The dW launch
+    splits an expert only when it is longer than a split threshold (about
+    1.25 workgroup shares of rows), into chunks of about half a share. The
+    counts are picked from the device's CU count so that one head expert is
+    split into many chunks, one expert is longer than a chunk but below the
+    threshold (so it stays one whole tile), and the rest are small or empty.
+    Every expert matches the oracle and the unsplit C-ABI call."""
+    from nanotitan_amd import capi
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    E, K, N = 64, 512, 256
+    small = [0 if e % 16 == 5 else 600 for e in range(E - 2)]
+    A0 = 20000 + 1100 + sum(small)
+    W = _ceil(A0 * _ceil(K, 128) * _ceil(N, 128), 2 * cus)
+    R = _ceil(max(_ceil(W, 2), 1024), 64) * 64
+    thr = max(_ceil(_ceil(5 * W, 4), 64) * 64, R)
+    mid = (R + thr) // 2 if thr > R + 1 else R  # longer than a chunk, not split
+    counts = [20000, mid] + small
+    assert counts[0] > thr and (thr == R or R < mid <= thr)
+    g = torch.Generator().manual_seed(23)
+    A = sum(counts)
+    X = torch.randn(A, K, generator=g).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    lib = capi.load()
+    code = capi.NT_BF16 if dtype == torch.bfloat16 else capi.NT_F16
+    Xg, Gg, og = X.cuda(), G.cuda(), offsets.cuda()
+    a = ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg)
+    c = torch.empty_like(a)
+    st = lib.nt_grouped_gemm_dw(code, Xg.data_ptr(), og.data_ptr(), Gg.data_ptr(), E, A, K, N,
+                                c.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert st == 0
+    want = O.grouped_gemm_dw(X, offsets, G)
+    check(a, want, dtype, scale=max(counts) ** 0.5)
+    check(c, want, dtype, scale=max(counts) ** 0.5)
+    # Unsplit experts are reduced in the same order either way.
+    for e in range(1, E):
+        assert torch.equal(a[e], c[e]), e
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("K,N", [(1032, 1000), (1000, 1032)])
 def test_split_duty_tiles_ragged(ext, dtype, K, N):
@@ -220,8 +268,8 @@ def test_split_duty_tiles_ragged(ext, dtype, K, N):
                                         ([20000, 0, 3, 9000, 5000], 1024, 256),
                                         ([5, 0, 17], 64, 128)])
 def test_paired_dw_dx_matches_separate_calls(ext, dtype, counts, K, N):
-    """bwd_grouped_gemm_dW_dX[_gelu]: the dW runs beside the dX on a second
-    stream when it has few 256x256 tiles (the first three cases; the third
+    """bwd_grouped_gemm_dW_dX[_gelu]: the dW runs beside the dX in one
+    launch when it has few 256x256 tiles (the first three cases; the third
     also splits its head expert's reduction), else after it. Outputs equal
     the separate calls bit for bit, and work queued next on the current
     stream sees them complete."""
@@ -238,7 +286,7 @@ def test_paired_dw_dx_matches_separate_calls(ext, dtype, counts, K, N):
     dW_ref = ext.bwd_grouped_gemm_dW_kernel(X, og, dOut)
     dX_ref = ext.bwd_grouped_gemm_dX_kernel(W, og, dOut)
     dH_ref = ext.bwd_grouped_gemm_dX_gelu(W, og, dOut, act_grad)
-    for _ in range(2):  # the second call reuses the side stream and its events
+    for _ in range(2):  # the second call reuses the caching allocator's workspace
         dW, dX = ext.bwd_grouped_gemm_dW_dX(X, W, og, dOut)
         same = torch.equal(dW.view(torch.int16), dW_ref.view(torch.int16)) and \
             torch.equal(dX.view(torch.int16), dX_ref.view(torch.int16))
