@@ -10,14 +10,16 @@ E=8, top-2, FFN 512->2048->512, bf16), synthetic seeded data, random-init
 weights.
 
 Prints ONE JSON line. ``value`` times K steps with only the step's own
-launches on the stream. ``roofline`` is for the dominant kernel family (the
+launches on the stream, after W warmup steps launched the same way (the
+GPU's clocks settle over the first ~20 back-to-back steps; the default W
+is past that). ``roofline`` is for the dominant kernel family (the
 grouped GEMMs): algorithmic FLOPs per launch (2*A*K*N) over the average
 launch duration, measured with HIP events on the launch stream around every
 launch in a second timed pass over the same K steps (the event markers
 slow the step by a few percent, so that pass does not feed ``value``). ``cpu_baseline`` times the CPU restatement of the reference
 torch path on a bounded token sample (rank 0, N=1 only).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2]
 """
 
 from __future__ import annotations
@@ -261,8 +263,8 @@ def cpu_baseline(cfg_id: int, budget_s: float = 20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
