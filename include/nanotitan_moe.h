@@ -203,10 +203,12 @@ int nt_route_topk_backward(const float* gates, const int32_t* topk, const float*
 
 /* ------------------------------------------------------------- grouped GEMM */
 
-/* Workspace for nt_grouped_gemm_dw with these sizes (the forward and dX
- * GEMMs need none; pass NULL, 0). It holds fp32 partial sums of experts whose
- * reduction is split (skewed routing) and is at most 64 MiB; 0 when no split
- * can occur. A smaller or NULL workspace is accepted: dW then runs unsplit. */
+/* Workspace for nt_grouped_gemm_dw and the paired dW + dX calls with these
+ * sizes (the forward and dX GEMMs need none; pass NULL, 0). It holds 256
+ * bytes of tile counters (paired calls), then the fp32 partial sums of
+ * experts whose reduction is split (skewed routing): at most 256 MiB plus
+ * one K*N*4 slab; 256 bytes when no split can occur. A smaller or NULL
+ * workspace is accepted: dW then runs unsplit (and unpaired). */
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N);
 
 /* out[a,:] = X[a,:] @ W[e] for a in [offsets[e], offsets[e+1]), float32
@@ -281,11 +283,12 @@ int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t
                         int64_t N, void* dX, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* dW[e] = X_e^T @ dOut_e summed over the rows of expert e (zero for an empty
- * expert). X [A,K], dOut [A,N], dW [E,K,N]. An expert with more rows than a
- * chunk (at least twice the mean expert size) is reduced in chunks whose
- * fp32 partials go to ws and are summed in chunk order by a second kernel,
- * so skewed routing spreads over the GPU. Deterministic: fixed chunks, fixed
- * summation order, no atomics.
+ * expert). X [A,K], dOut [A,N], dW [E,K,N]. An expert with more rows than
+ * about 1.25 times a workgroup's share of the reduction (skewed routing) is
+ * reduced in chunks of about half a share, whose fp32 partials go to ws and
+ * are summed in chunk order by a second kernel, so no single tile outlasts
+ * the rest. Deterministic: the chunks depend only on the sizes and the
+ * device's CU count, fixed summation order, no atomics.
  * Replaces bwd_grouped_gemm_dW_kernel (reference csrc/kernels/bwd_grouped_gemm_dW.cu:43-86). */
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,
