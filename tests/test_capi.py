@@ -105,3 +105,63 @@ def test_workspace_sizes_are_sane():
 def test_argument_errors_return_codes(fn, args, code):
     lib = capi.load()
     assert getattr(lib, fn)(*args) == code
+
+
+C_HOST = r"""
+#include <stdio.h>
+#include "nanotitan_moe.h"
+
+/* The GELU-FFN layer sequence of the integration guide, compiled against the
+   header only (never called here: there is no GPU on this machine). */
+int layer(const float* logits, const void* X, int64_t T, int32_t E, int32_t k, int64_t d,
+          int64_t f, const void* W_up, const void* W_down, float* gates, int32_t* topk,
+          int32_t* counts, int32_t* offsets, void* packed_X, int32_t* token_id,
+          int32_t* expert, float* packed_w, int32_t* inv, void* act, void* g, void* y,
+          void* out, void* ws, size_t ws_bytes, hipStream_t stream) {
+  int32_t TB = nt_dispatch_block_tokens(T, k, d, NT_BF16);
+  int rc = nt_route_topk_count(logits, T, E, k, gates, topk, NULL, TB, (int32_t*)ws, stream);
+  if (rc == NT_OK)
+    rc = nt_dispatch_counted(NT_BF16, X, gates, topk, T, k, d, E, counts, offsets, packed_X,
+                             token_id, expert, packed_w, inv, ws, ws_bytes, stream);
+  if (rc == NT_OK)
+    rc = nt_grouped_gemm_gelu(NT_BF16, packed_X, offsets, W_up, E, T * k, d, f, act, g, NULL, 0,
+                              stream);
+  if (rc == NT_OK)
+    rc = nt_grouped_gemm(NT_BF16, act, offsets, W_down, E, T * k, f, d, y, NULL, 0, stream);
+  if (rc == NT_OK) rc = nt_combine_inv(NT_BF16, y, inv, packed_w, T, k, d, NT_BF16, out, stream);
+  return rc;
+}
+
+int main(void) {
+  printf("%d|%s|%zu\n", nt_version(), nt_strerror(NT_ERR_WORKSPACE),
+         nt_dispatch_workspace_bytes(30720, 2, 8, 512, NT_BF16));
+  return 0;
+}
+"""
+
+
+def test_plain_c_host_compiles_links_and_runs(tmp_path):
+    """A C99 host (gcc, no HIP compiler, no C++) compiles against the header,
+    links libnanotitan_moe.so and calls its host-only functions; the layer
+    sequence of the integration guide type-checks against the header."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    gcc = shutil.which("gcc")
+    rocm_inc = Path("/opt/rocm/include")
+    if gcc is None or not (rocm_inc / "hip").is_dir():
+        pytest.skip("gcc or the HIP headers are not available")
+    src = tmp_path / "host.c"
+    src.write_text(C_HOST)
+    lib_dir = ROOT / "nanotitan_amd"
+    exe = tmp_path / "host"
+    cmd = [gcc, "-std=c99", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{rocm_inc}",
+           f"-I{ROOT / 'include'}", str(src), f"-L{lib_dir}", "-lnanotitan_moe",
+           f"-Wl,-rpath,{lib_dir}", "-o", str(exe)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.strip()
+    version, message, ws = out.split("|")
+    assert int(version) == capi.load().nt_version()
+    assert message == capi.load().nt_strerror(capi.NT_ERR_WORKSPACE).decode()
+    assert int(ws) == capi.load().nt_dispatch_workspace_bytes(30720, 2, 8, 512, capi.NT_BF16)
