@@ -376,6 +376,20 @@ def main():
             roofline["traffic_algorithmic"] = round(
                 sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
             roofline["traffic_source"] = f"profiles/{prof.name}"
+    # MFMA busy fraction and running clock of the GEMMs, from a rocprofv3
+    # counter pass (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x 1024
+    # SIMDs) committed with the profile summaries; time-weighted over the
+    # GEMM families of a step.
+    mf = ROOT / "profiles" / f"mfma_{wl['name'].lower()}.json"
+    if mf.exists():
+        fam_m = json.loads(mf.read_text())
+        t_all = sum(v["launches"] * v["avg_us"] for v in fam_m.values())
+        if t_all > 0:
+            def tw(key):
+                return sum(v[key] * v["launches"] * v["avg_us"] for v in fam_m.values()) / t_all
+            roofline["mfma_busy_frac"] = round(tw("mfma_busy_frac"), 4)
+            roofline["clock_ghz"] = round(tw("clock_ghz"), 3)
+            roofline["mfma_source"] = f"profiles/{mf.name}"
     kernels = {}
     for fam, r in fams.items():
         avg_ms = r["ms"] / r["launches"]
