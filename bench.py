@@ -19,7 +19,10 @@ launch in a second timed pass over the same K steps (the event markers
 slow the step by a few percent, so that pass does not feed ``value``). ``cpu_baseline`` times the CPU restatement of the reference
 torch path on a bounded token sample (rank 0, N=1 only).
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2] [--ffn gelu|swiglu]
+
+``--ffn swiglu`` runs the reference's SwiGLU ExpertFFN in place of the
+configs' GELU FFN (a secondary figure; the headline is the GELU FFN).
 """
 
 from __future__ import annotations
@@ -90,6 +93,11 @@ class LaunchTimer:
         "bwd_grouped_gemm_dW_kernel": "gemm",
         "bwd_grouped_gemm_dW_dX": "gemm",
         "bwd_grouped_gemm_dW_dX_gelu": "gemm",
+        "grouped_gemm_swiglu": "gemm",
+        "bwd_grouped_gemm_dX_swiglu": "gemm",
+        "bwd_grouped_gemm_dW_dX_swiglu": "gemm",
+        "bwd_grouped_gemm_dW_dX2": "gemm",
+        "bwd_grouped_gemm_dX2": "gemm",
         "dispatch_tokens": "dispatch",
         "dispatch_tokens_counted": "dispatch",
         "combine_inv": "combine_fwd",
@@ -123,9 +131,14 @@ class LaunchTimer:
 
     @staticmethod
     def _launches(name):
-        """GEMM launches inside one call (the paired dW + dX calls hold two,
-        which may run side by side: the pair's span is their joint time)."""
-        return 2 if name in ("bwd_grouped_gemm_dW_dX", "bwd_grouped_gemm_dW_dX_gelu") else 1
+        """GEMMs inside one call (the paired dW + dX calls hold two, which may
+        run side by side: the pair's span is their joint time). SwiGLU: the
+        gate|value forward and the two-part dX (reduction over gate and value)
+        count as two GEMMs each, the dW_gate + two-part dX pair as three."""
+        if name in ("bwd_grouped_gemm_dW_dX", "bwd_grouped_gemm_dW_dX_gelu", "grouped_gemm_swiglu",
+                    "bwd_grouped_gemm_dW_dX_swiglu", "bwd_grouped_gemm_dX2"):
+            return 2
+        return 3 if name == "bwd_grouped_gemm_dW_dX2" else 1
 
     @staticmethod
     def _work(name, args):
@@ -136,6 +149,21 @@ class LaunchTimer:
         if name in ("bwd_grouped_gemm_dX_kernel", "bwd_grouped_gemm_dX_gelu"):
             W, _off, G = args[:3]
             return 2.0 * G.shape[0] * W.shape[1] * W.shape[2]
+        if name == "grouped_gemm_swiglu":  # X [A,d], W_gate, W_val [E,d,f]
+            X, _off, Wg = args[:3]
+            return 2 * 2.0 * X.shape[0] * X.shape[1] * Wg.shape[2]
+        if name == "bwd_grouped_gemm_dX_swiglu":  # W_out [E,f,d], dy [A,d]
+            W, _off, G = args[:3]
+            return 2.0 * G.shape[0] * W.shape[1] * W.shape[2]
+        if name == "bwd_grouped_gemm_dW_dX_swiglu":  # hidden [A,f], dy [A,d]
+            h, _W, _off, G = args[:4]
+            return 2 * 2.0 * h.shape[0] * h.shape[1] * G.shape[1]
+        if name in ("bwd_grouped_gemm_dW_dX2", "bwd_grouped_gemm_dX2"):
+            # two-part dX over the gate|value reduction (+ dW_gate when paired)
+            Wg = args[1] if name == "bwd_grouped_gemm_dW_dX2" else args[0]
+            dg = args[-2]
+            E, d, f = Wg.shape
+            return (3 if name == "bwd_grouped_gemm_dW_dX2" else 2) * 2.0 * dg.shape[0] * d * f
         if name == "bwd_grouped_gemm_dW_kernel":
             X, _off, G = args
             return 2.0 * X.shape[0] * X.shape[1] * G.shape[1]
@@ -200,6 +228,19 @@ class _GeluFFN(torch.nn.Module):
         from nanotitan_amd.moe_ops import grouped_gelu_ffn_fn
 
         return grouped_gelu_ffn_fn(packed_X, self.W_up, self.W_down, offsets)
+
+
+class _SwiGLUFFN(torch.nn.Module):
+    """The reference's ExpertFFN (src/model/feed_fwd.py:102-112): silu(X W_gate) * (X W_val), then W_out."""
+
+    def __init__(self, W_gate, W_val, W_out):
+        super().__init__()
+        self.W_gate, self.W_val, self.W_out = W_gate, W_val, W_out
+
+    def forward(self, packed_X, offsets):
+        from nanotitan_amd.moe_ops import swiglu_ffn_fn
+
+        return swiglu_ffn_fn(packed_X, self.W_gate, self.W_val, self.W_out, offsets)
 
 
 def cpu_model() -> str:
@@ -268,6 +309,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--ffn", choices=["gelu", "swiglu"], default="gelu",
+                    help="expert FFN: the configs' up->GELU->down (headline) or the reference's "
+                         "SwiGLU ExpertFFN")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 1 GiB (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -308,10 +352,19 @@ def main():
     W_up = wl["W_up"].detach().requires_grad_(True)
     W_down = wl["W_down"].detach().requires_grad_(True)
     ffn = _GeluFFN(W_up, W_down)
+    W_val = None
+    if args.ffn == "swiglu":  # W_up serves as W_gate and W_down as W_out
+        std = WORKLOADS[args.config][7]
+        g = torch.Generator(device="cuda").manual_seed(4321)
+        W_val = (torch.randn(W_up.shape, generator=g, device="cuda") * std).to(wl["dtype"])
+        W_val.requires_grad_(True)
+        ffn = _SwiGLUFFN(W_up, W_val, W_down)
 
     for _ in range(args.warmup):
         gpu_step(wl, W_up, W_down, ffn)
         W_up.grad = W_down.grad = None
+        if W_val is not None:
+            W_val.grad = None
     torch.cuda.synchronize()
 
     # Headline: K steps with nothing but the step's own launches on the stream.
@@ -320,6 +373,8 @@ def main():
     for _ in range(args.steps):
         gpu_step(wl, W_up, W_down, ffn)
         W_up.grad = W_down.grad = None
+        if W_val is not None:
+            W_val.grad = None
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
@@ -332,6 +387,8 @@ def main():
     for _ in range(args.steps):
         gpu_step(wl, W_up, W_down, ffn)
         W_up.grad = W_down.grad = None
+        if W_val is not None:
+            W_val.grad = None
     torch.cuda.synchronize()
     elapsed_events = time.perf_counter() - t1
     timer.active = False
@@ -359,7 +416,7 @@ def main():
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
     # (calibrated on a device copy), committed with the profile summaries.
     prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
-    if prof.exists():
+    if prof.exists() and args.ffn == "gelu":
         fams_t = json.loads(prof.read_text()).get("families", {})
         # GEMM launches of one step: up (fused GELU), down, and the backward's
         # down dX (fused GELU backward), up dX and two dW, either as paired
@@ -381,7 +438,7 @@ def main():
     # SIMDs) committed with the profile summaries; time-weighted over the
     # GEMM families of a step.
     mf = ROOT / "profiles" / f"mfma_{wl['name'].lower()}.json"
-    if mf.exists():
+    if mf.exists() and args.ffn == "gelu":
         fam_m = json.loads(mf.read_text())
         t_all = sum(v["launches"] * v["avg_us"] for v in fam_m.values())
         if t_all > 0:
@@ -416,7 +473,8 @@ def main():
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,std^2) random-init expert weights)",
         "config": {
             "workload": f"{wl['name']}: MoE layer fwd+bwd, {wl['T']} tokens x d={wl['d']}, "
-                        f"E={wl['E']}, top-{wl['k']}, FFN {wl['d']}->{wl['f']}->{wl['d']} GELU",
+                        f"E={wl['E']}, top-{wl['k']}, FFN {wl['d']}->{wl['f']}->{wl['d']} "
+                        + ("GELU" if args.ffn == "gelu" else "SwiGLU (reference ExpertFFN)"),
             "tokens": wl["T"],
             "d_model": wl["d"],
             "num_experts": wl["E"],
