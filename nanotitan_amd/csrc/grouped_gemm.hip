@@ -75,15 +75,42 @@ __device__ void build_m_prefix(const int32_t* __restrict__ offsets, int E, int64
 // written, as zeros). s_pref[e] = chunks of experts < e; s_split[e] = chunks
 // of experts < e that have at least two (those write fp32 partials, one slab
 // per chunk, and a reduce pass sums them in chunk order). R = 0 means one
-// chunk per expert. Ends with a workgroup barrier.
+// chunk per expert.
+//
+// The workspace holds `cap` slabs, enough whenever the experts' row ranges
+// are disjoint (non-decreasing offsets). expert_rows clamps each expert on
+// its own, so a non-monotone offsets array can give ranges that overlap and
+// more split chunks than that; then every expert is one chunk (no partial
+// slab is written, and split_total() tells the reduce pass to do nothing).
+// Ends with a workgroup barrier.
 __device__ __forceinline__ int dw_chunks(int64_t rows, int32_t R, int32_t thr) {
   if (R <= 0 || rows <= thr) return 1;
   return (int)ceil_div(rows, R);
 }
+// Wave-wide: chunks of the split experts (those with two or more) over all
+// E experts, the same on every lane.
+__device__ int split_total(const int32_t* __restrict__ offsets, int E, int64_t A, int32_t R,
+                           int32_t thr) {
+  int tot = 0;
+  for (int s = 0; s < E; s += kWave) {
+    const int e = s + lane_id();
+    int v = 0;
+    if (e < E) {
+      int64_t a, b;
+      expert_rows(offsets, e, A, a, b);
+      v = dw_chunks(b - a, R, thr);
+      v = v >= 2 ? v : 0;
+    }
+    tot += wave_sum_int(v);
+  }
+  return tot;
+}
 __device__ void build_chunk_prefix(const int32_t* __restrict__ offsets, int E, int64_t A,
-                                   int32_t R, int32_t thr, int32_t* s_pref, int32_t* s_split) {
+                                   int32_t R, int32_t thr, int32_t cap, int32_t* s_pref,
+                                   int32_t* s_split) {
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
+    if (R > 0 && split_total(offsets, E, A, R, thr) > cap) R = 0;
     int carry = 0, carry_s = 0;
     for (int s = 0; s < E; s += kWave) {
       const int e = s + lane;
@@ -401,6 +428,7 @@ struct GemmArgs {
   void* out3;
   const void* aux2;
   int32_t split_thr;  // dW: experts with more rows than this are split (when chunk > 0)
+  int32_t slab_cap;   // dW: partial slabs the workspace holds (when chunk > 0)
 };
 
 // Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
@@ -1082,7 +1110,7 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
     build_m_prefix(g.offsets, g.E, g.A, BM, s_pref);
     mtiles = s_pref[g.E];
   } else {
-    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, g.split_thr, s_pref,
+    build_chunk_prefix(g.offsets, g.E, g.A, g.chunk, g.split_thr, g.slab_cap, s_pref,
                        s_pref + (NT_MAX_EXPERTS + 1));
     mtiles = (int64_t)s_pref[g.E] * g.ntm;
   }
@@ -1682,7 +1710,7 @@ int launch_swiglu_elementwise(int dtype, void* io, void* dg, const void* g, cons
 template <typename T>
 __global__ void __launch_bounds__(256)
 dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int32_t R,
-                 int32_t thr,
+                 int32_t thr, int32_t cap,
                  const float* __restrict__ partial, int64_t KN,
                  typename elem<T>::storage* __restrict__ dW) {
   __shared__ int32_t s_info[2];
@@ -1695,6 +1723,9 @@ dw_reduce_kernel(const int32_t* __restrict__ offsets, int32_t E, int64_t A, int3
     if (dw_chunks(b - a, R, thr) < 2) return;
   }
   if (threadIdx.x < kWave) {
+    // More split chunks than slabs (overlapping expert ranges): the GEMM
+    // ran every expert unsplit (build_chunk_prefix) and wrote dW itself.
+    if (split_total(offsets, E, A, R, thr) > cap) R = 0;
     const int lane = lane_id();
     int before = 0;
     for (int s0 = 0; s0 < e; s0 += kWave) {
@@ -1904,13 +1935,14 @@ int dx_impl(int dtype, const void* W, const int32_t* offsets, const void* dOut,
 int launch_dw_reduce(int dtype, const int32_t* offsets, int32_t E, int64_t A, int64_t K,
                      int64_t N, DwSplit sp, const float* partial, void* dW, hipStream_t stream) {
   const int64_t KN = K * N;
+  const int32_t cap = (int32_t)dw_slabs(A, sp);
   const dim3 grid((unsigned)std::min<int64_t>(ceil_div(KN, 256 * 8), 64), (unsigned)E);
   if (dtype == NT_BF16)
     hipLaunchKernelGGL((dw_reduce_kernel<bf16>), grid, dim3(256), 0, stream, offsets, E, A, sp.R,
-                       sp.thr, partial, KN, static_cast<uint16_t*>(dW));
+                       sp.thr, cap, partial, KN, static_cast<uint16_t*>(dW));
   else
     hipLaunchKernelGGL((dw_reduce_kernel<f16>), grid, dim3(256), 0, stream, offsets, E, A, sp.R,
-                       sp.thr, partial, KN, static_cast<uint16_t*>(dW));
+                       sp.thr, cap, partial, KN, static_cast<uint16_t*>(dW));
   return launch_status();
 }
 
@@ -1930,6 +1962,7 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
   if (split) {
     g.chunk = sp.R;
     g.split_thr = sp.thr;
+    g.slab_cap = (int32_t)dw_slabs(A, sp);
     g.partial = partial;
   }
   const int st = dw_big_tiles(A, K, N, E)
@@ -1983,6 +2016,7 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   if (split) {
     gw.chunk = sp.R;
     gw.split_thr = sp.thr;
+    gw.slab_cap = (int32_t)dw_slabs(A, sp);
     gw.partial = partial;
   }
   int32_t* dyn = static_cast<int32_t*>(ws);

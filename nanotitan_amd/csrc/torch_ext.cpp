@@ -61,6 +61,13 @@ void check_f32(const Tensor& t, const char* name) {
   check_device(t, name);
 }
 
+// Every tensor of one call lives on the device of the first.
+void check_same_device(const Tensor& first, std::initializer_list<const Tensor*> rest) {
+  for (const Tensor* t : rest)
+    TORCH_CHECK(t->device() == first.device(), "all tensors must be on the same device (",
+                first.device(), " vs ", t->device(), ")");
+}
+
 hipStream_t stream_of(const Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.get_device()).stream();
 }
@@ -648,6 +655,10 @@ Tensor combine_inv(Tensor y, Tensor inv, Tensor w, c10::ScalarType out_dtype) {
   check_i32(inv, "inv");
   check_f32(w, "packed_topk_weights");
   TORCH_CHECK(y.dim() == 2 && inv.dim() == 2, "expected y [A,d], inv [T,k]");
+  // The kernels read rows p < T*k of y and w (and skip larger entries of inv).
+  TORCH_CHECK(y.size(0) == inv.numel() && w.numel() == inv.numel(),
+              "expert_outputs and packed_topk_weights must have T*k = inv.numel() rows");
+  check_same_device(y, {&inv, &w});
   const int64_t T = inv.size(0), k = inv.size(1), d = y.size(1);
   c10::hip::HIPGuard guard(y.get_device());
   Tensor out = at::empty({T, d}, y.options().dtype(out_dtype));
@@ -671,6 +682,10 @@ std::tuple<Tensor, Tensor> combine_backward_inv(Tensor y, Tensor inv, Tensor w, 
               "expected y [A,d], inv [T,k], grad [T,d]");
   TORCH_CHECK(dY.scalar_type() == at::kFloat || dY.scalar_type() == y.scalar_type(),
               "grad must be float32 or the activation dtype");
+  // The kernel reads and writes rows p < T*k of y, dy, w and dw.
+  TORCH_CHECK(y.size(0) == inv.numel() && w.numel() == inv.numel(),
+              "expert_outputs and packed_topk_weights must have T*k = inv.numel() rows");
+  check_same_device(y, {&inv, &w, &dY});
   const int64_t T = inv.size(0), k = inv.size(1), d = y.size(1);
   c10::hip::HIPGuard guard(y.get_device());
   Tensor dy = at::empty_like(y);
@@ -690,6 +705,10 @@ std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv)
   check_f32(dpw, "packed_topk_weights_grad");
   check_i32(inv, "inv");
   TORCH_CHECK(dpX.dim() == 2 && inv.dim() == 2, "expected packed_X_grad [A,d], inv [T,k]");
+  // The kernel reads rows p < T*k of dpX and dpw.
+  TORCH_CHECK(dpX.size(0) == inv.numel() && dpw.numel() == inv.numel(),
+              "packed_X_grad and packed_topk_weights_grad must have T*k = inv.numel() rows");
+  check_same_device(dpX, {&dpw, &inv});
   const int64_t T = inv.size(0), k = inv.size(1), d = dpX.size(1);
   c10::hip::HIPGuard guard(dpX.get_device());
   Tensor dX = at::empty({T, d}, dpX.options());

@@ -201,3 +201,24 @@ def test_inverse_map_kernels_with_dropped_slots(ext, k, dtype):
     dX, dw2 = ext.pack_backward_inv(dpX.cuda(), dpw.cuda(), inv.cuda())
     assert torch.equal(bits(dX), bits(want_dX))
     assert torch.equal(bits(dw2), bits(torch.from_numpy(want_dw2)))
+
+
+def test_inverse_map_ops_check_row_counts(ext):
+    """The inverse-map ops read rows p < T*k of their packed inputs: a tensor
+    with another row count is rejected before any launch."""
+    T, k, d = 16, 2, 8
+    inv = torch.arange(T * k, dtype=torch.int32, device="cuda").view(T, k)
+    y = torch.randn(T * k, d, device="cuda")
+    w = torch.rand(T * k, device="cuda")
+    dY = torch.randn(T, d, device="cuda")
+    short_y, short_w = y[: T * k - 1].contiguous(), w[: T * k - 1].contiguous()
+    for call in (lambda: ext.combine_inv(short_y, inv, w, torch.float32),
+                 lambda: ext.combine_inv(y, inv, short_w, torch.float32),
+                 lambda: ext.combine_backward_inv(short_y, inv, w, dY),
+                 lambda: ext.combine_backward_inv(y, inv, short_w, dY),
+                 lambda: ext.pack_backward_inv(short_y, w, inv),
+                 lambda: ext.pack_backward_inv(y, short_w, inv)):
+        with pytest.raises(RuntimeError, match=r"inv\.numel\(\)"):
+            call()
+    with pytest.raises(RuntimeError, match="GPU tensor|same device"):
+        ext.combine_inv(y, inv, w.cpu(), torch.float32)

@@ -359,3 +359,30 @@ def test_paired_calls_edge_cases(ext, dtype, counts, K, N):
     check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(max(counts), 1) ** 0.5)
     if A:
         check(dX, O.grouped_gemm_dx(W, offsets, G), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16])
+def test_dw_non_monotone_offsets_stay_in_the_workspace(ext, dtype):
+    """Offsets [0, A, 0, A, ...]: each expert's range is clamped on its own, so
+    experts 0, 2, 4, 6 each span all A rows and 1, 3, 5, 7 none. At these sizes
+    the dW split would cut every full expert into chunks (64 in all), more than
+    the workspace's 32 partial slabs; the kernels then run every expert
+    unsplit. dW[e] = X^T dOut over the expert's clamped range, for the plain
+    and the paired (dW beside dX) calls alike."""
+    A, K, N, E = 16384, 256, 1024, 8
+    g = torch.Generator().manual_seed(77)
+    X = torch.randn(A, K, generator=g).to(dtype)
+    G = torch.randn(A, N, generator=g).to(dtype)
+    W = (torch.randn(E, K, N, generator=g) / 16).to(dtype)
+    offsets = torch.tensor([0 if e % 2 == 0 else A for e in range(E + 1)], dtype=torch.int32)
+    Xg, Gg, Wg, og = X.cuda(), G.cuda(), W.cuda(), offsets.cuda()
+    dW = ext.bwd_grouped_gemm_dW_kernel(Xg, og, Gg)
+    dW2, _dX = ext.bwd_grouped_gemm_dW_dX(Xg, Wg, og, Gg)
+    torch.cuda.synchronize()
+    full = (X.float().t() @ G.float()).double()
+    for e in range(E):
+        if e % 2 == 0:
+            check(dW[e], full, dtype, scale=A ** 0.5)
+        else:
+            assert not dW[e].cpu().any(), e
+    assert torch.equal(dW.cpu().view(torch.int16), dW2.cpu().view(torch.int16))
