@@ -56,7 +56,8 @@ enum nt_status {
   NT_ERR_TOO_MANY_EXPERTS = 3, /* E above NT_MAX_EXPERTS */
   NT_ERR_WORKSPACE = 4,     /* workspace missing or smaller than *_workspace_bytes() */
   NT_ERR_LAUNCH = 5,        /* a kernel launch failed (hipGetLastError) */
-  NT_ERR_TOO_LARGE = 6      /* a size exceeds what the kernels index (e.g. > 2^31-1 rows) */
+  NT_ERR_TOO_LARGE = 6,     /* a size exceeds what the kernels index (e.g. > 2^31-1 rows) */
+  NT_ERR_SCRATCH = 7        /* a no-allocation call needs more than its fixed scratch */
 };
 
 #define NT_MAX_EXPERTS 1024
@@ -118,6 +119,26 @@ int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t*
                         int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
                         void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
                         int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Bytes of device scratch the library owns for nt_dispatch_noalloc, per GPU. */
+#define NT_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* nt_dispatch without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference: its dispatch
+ * allocates through torch. The workspace lives in a fixed device array of
+ * NT_NOALLOC_SCRATCH_BYTES that the library owns on each GPU it runs on
+ * (held until the process ends); sizes whose nt_dispatch_workspace_bytes
+ * exceed it return NT_ERR_SCRATCH before any launch (about T/16 * E * 4
+ * bytes at 4 KiB rows: 65536 tokens x 128 experts fit). Calls on one GPU
+ * share that array and leave its contents behind (nothing in it needs to
+ * start at zero); two calls that overlap on one GPU (different streams,
+ * not ordered) race on it. Same outputs as nt_dispatch, bit for bit, and no
+ * hipMalloc, hipFree or allocating library call. */
+int nt_dispatch_noalloc(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                        int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                        void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                        int32_t* inv, hipStream_t stream);
 
 /* ------------------------------------------------------------------- combine */
 

@@ -22,7 +22,9 @@ NT_ERR_TOO_MANY_EXPERTS = 3
 NT_ERR_WORKSPACE = 4
 NT_ERR_LAUNCH = 5
 NT_ERR_TOO_LARGE = 6
+NT_ERR_SCRATCH = 7
 NT_MAX_EXPERTS = 1024
+NT_NOALLOC_SCRATCH_BYTES = 4 << 20
 
 _P = c_void_p  # any device pointer, hipStream_t included
 
@@ -48,6 +50,10 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_int, _P, _P, _P, c_int64, c_int32, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P,
          c_size_t, _P],
+    ),
+    "nt_dispatch_noalloc": (
+        c_int,
+        [c_int, _P, _P, _P, c_int64, c_int32, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P],
     ),
     "nt_dispatch_block_tokens": (c_int32, [c_int64, c_int32, c_int64, c_int]),
     "nt_combine_workspace_bytes": (c_size_t, [c_int64, c_int64]),

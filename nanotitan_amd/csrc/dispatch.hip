@@ -17,6 +17,8 @@
 // Packed order is the stable counting sort of the flat assignment index by
 // expert: exactly the order of the reference torch backend
 // (src/model/torch_backend.py:58-66), deterministic run to run.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace nt {
@@ -460,6 +462,73 @@ int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t*
                         int32_t* inv, void* ws, size_t ws_bytes, hipStream_t stream) {
   return dispatch_impl(dtype, X, w, topk, T, k, d, E, counts, offsets, packed_X, token_id,
                        expert, packed_w, inv, ws, ws_bytes, true, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------ no-allocation dispatch
+//
+// nt_dispatch with its workspace (the per-block expert histogram and the
+// per-expert bases, dispatch_ws_bytes) in a device array the library owns,
+// for callers that cannot allocate: code under graph capture, tight serving
+// loops. Each GPU the library runs on holds its own copy of the array until
+// the process ends. Every call on a GPU shares that GPU's copy and leaves its
+// contents behind; nothing in it needs to start at zero (the histogram kernel
+// writes every entry the scan and the pack read), but two calls that overlap
+// on one GPU (different streams, no ordering between them) race on it.
+static __device__ __align__(256) unsigned char scratch[NT_NOALLOC_SCRATCH_BYTES];
+
+namespace nt {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to. The
+// array's host-side name is only a handle: the address comes from
+// hipGetSymbolAddress, called once per device with that device current.
+int scratch_on(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return NT_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return NT_ERR_LAUNCH;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return NT_ERR_LAUNCH;
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (err != hipSuccess || ptr == nullptr) return NT_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NT_OK;
+}
+
+}  // namespace
+}  // namespace nt
+
+extern "C" {
+
+int nt_dispatch_noalloc(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
+                        int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
+                        void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
+                        int32_t* inv, hipStream_t stream) {
+  int st = check_common(T, k, E);
+  if (st != NT_OK) return st;
+  const int eb = dtype_bytes(dtype);
+  if (eb == 0) return NT_ERR_DTYPE;
+  if (d < 0) return NT_ERR_INVALID_ARG;
+  // The same workspace nt_dispatch would take; beyond the array it is an error.
+  const size_t need = dispatch_ws_bytes(plan_pack(T, k, d * eb), E);
+  if (need > (size_t)NT_NOALLOC_SCRATCH_BYTES) return NT_ERR_SCRATCH;
+  void* ws = nullptr;
+  st = scratch_on(stream, &ws);
+  if (st != NT_OK) return st;
+  return dispatch_impl(dtype, X, w, topk, T, k, d, E, counts, offsets, packed_X, token_id, expert,
+                       packed_w, inv, ws, (size_t)NT_NOALLOC_SCRATCH_BYTES, false, stream);
 }
 
 }  // extern "C"

@@ -12,6 +12,8 @@ const char* nt_strerror(int code) {
     case NT_ERR_WORKSPACE: return "workspace missing or too small";
     case NT_ERR_LAUNCH: return "HIP kernel launch failed";
     case NT_ERR_TOO_LARGE: return "size exceeds the 32-bit row/index range of the kernels";
+    case NT_ERR_SCRATCH:
+      return "sizes need more workspace than the no-allocation scratch (NT_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status code";
   }
 }
