@@ -5,8 +5,10 @@ Two artefacts, both next to this file:
 * ``libnanotitan_moe.so`` — the C ABI (``include/nanotitan_moe.h``): every HIP
   kernel, compiled by ``hipcc --offload-arch=gfx950``. No torch dependency.
 * ``_nanotitan_hip.so`` — the PyTorch-ROCm extension module exposing the
-  reference op surface (``csrc/torch_ext.cpp``), compiled by ``g++`` against
-  torch's headers and linked to the C ABI library through ``$ORIGIN``.
+  reference op surface (``csrc/torch_ext.cpp``: the pybind module and the
+  ``torch.ops.nanotitan`` op library, whose CPU kernels are
+  ``csrc/cpu_ops.cpp``), compiled by ``g++`` against torch's headers and
+  linked to the C ABI library through ``$ORIGIN``.
 
 Plain compiler invocations (no hipify, no cpp_extension JIT), so the built
 files travel with the source tree. ``python -m nanotitan_amd.build`` rebuilds
@@ -99,7 +101,11 @@ def build_extension(verbose: bool = False) -> Path:
         "-std=c++17",
         "-fPIC",
         "-shared",
+        # The CPU kernels' ordered fp32 sums must round each product before
+        # the add, as the HIP kernels do.
+        "-ffp-contract=off",
         str(CSRC / "torch_ext.cpp"),
+        str(CSRC / "cpu_ops.cpp"),
         "-o",
         str(EXT.with_suffix(".so.tmp")),
         f"-I{INCLUDE}",

@@ -720,7 +720,238 @@ std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv)
   return {dX, dw};
 }
 
+// ------------------------------------------------------------ Meta kernels
+//
+// Output shapes and dtypes only (fake / meta tensors, torch.compile tracing):
+// every output's shape follows from the input shapes, none from their values.
+namespace meta {
+
+Tensor count_expert_kernel(Tensor topk, Tensor mask, int64_t num_experts, int64_t num_topk) {
+  return at::empty({num_experts}, topk.options().dtype(at::kInt));
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> pack_tokens_inv(Tensor X, Tensor w, Tensor topk,
+                                                                   Tensor cursor) {
+  const int64_t T = X.size(0), d = X.size(1), k = w.size(1), A = T * k;
+  auto i32 = X.options().dtype(at::kInt);
+  return {at::empty({A, d}, X.options()), at::empty({A}, i32), at::empty({A}, i32),
+          at::empty({A}, X.options().dtype(at::kFloat)), at::empty({T, k}, i32)};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> pack_tokens_kernel(Tensor X, Tensor w, Tensor topk,
+                                                              Tensor cursor) {
+  auto r = pack_tokens_inv(X, w, topk, cursor);
+  return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r)};
+}
+
+Tensor combine_tokens_kernel(Tensor y, Tensor token_id, Tensor w, int64_t num_tokens,
+                             int64_t d_model) {
+  return at::empty({num_tokens, d_model}, y.options().dtype(at::kFloat));
+}
+
+std::tuple<Tensor, Tensor> combine_kernel_backward(Tensor y, Tensor token_id, Tensor w, Tensor dY,
+                                                   int64_t hidden_dim) {
+  return {at::empty_like(y), at::empty(w.sizes(), w.options())};
+}
+
+std::tuple<Tensor, Tensor> pack_kernel_backward(Tensor dpX, Tensor dpw, Tensor token_id,
+                                                Tensor expert, Tensor topk) {
+  return {at::empty({topk.size(0), dpX.size(1)}, dpX.options()),
+          at::empty({topk.size(0), topk.size(1)}, dpw.options())};
+}
+
+Tensor grouped_gemm_kernel(Tensor X, Tensor offsets, Tensor W) {
+  return at::empty({X.size(0), W.size(2)}, X.options());
+}
+
+Tensor bwd_grouped_gemm_dW_kernel(Tensor X, Tensor offsets, Tensor dOut) {
+  return at::empty({offsets.size(0) - 1, X.size(1), dOut.size(1)}, X.options());
+}
+
+Tensor bwd_grouped_gemm_dX_kernel(Tensor W, Tensor offsets, Tensor dOut) {
+  return at::empty({dOut.size(0), W.size(1)}, W.options());
+}
+
+std::tuple<Tensor, Tensor> grouped_gemm_gelu(Tensor X, Tensor offsets, Tensor W) {
+  return {grouped_gemm_kernel(X, offsets, W), grouped_gemm_kernel(X, offsets, W)};
+}
+
+Tensor bwd_grouped_gemm_dX_gelu(Tensor W, Tensor offsets, Tensor dOut, Tensor act_grad) {
+  return bwd_grouped_gemm_dX_kernel(W, offsets, dOut);
+}
+
+std::tuple<Tensor, Tensor, Tensor> grouped_gemm_swiglu(Tensor X, Tensor offsets, Tensor Wg,
+                                                       Tensor Wv) {
+  return {grouped_gemm_kernel(X, offsets, Wg), grouped_gemm_kernel(X, offsets, Wg),
+          grouped_gemm_kernel(X, offsets, Wg)};
+}
+
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dX_swiglu(Tensor W, Tensor offsets, Tensor dOut,
+                                                      Tensor gate, Tensor value) {
+  return {bwd_grouped_gemm_dX_kernel(W, offsets, dOut), bwd_grouped_gemm_dX_kernel(W, offsets, dOut)};
+}
+
+Tensor bwd_grouped_gemm_dX2(Tensor W1, Tensor W2, Tensor offsets, Tensor dOut1, Tensor dOut2) {
+  return bwd_grouped_gemm_dX_kernel(W1, offsets, dOut1);
+}
+
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX(Tensor X, Tensor W, Tensor offsets, Tensor dOut) {
+  return {at::empty_like(W), at::empty_like(X)};
+}
+
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX_gelu(Tensor act, Tensor W, Tensor offsets,
+                                                       Tensor dOut, Tensor act_grad) {
+  return {at::empty_like(W), at::empty_like(act)};
+}
+
+std::tuple<Tensor, Tensor, Tensor> bwd_grouped_gemm_dW_dX_swiglu(Tensor hidden, Tensor W,
+                                                                 Tensor offsets, Tensor dOut,
+                                                                 Tensor gate, Tensor value) {
+  return {at::empty_like(W), at::empty_like(hidden), at::empty_like(hidden)};
+}
+
+std::tuple<Tensor, Tensor> bwd_grouped_gemm_dW_dX2(Tensor X, Tensor W1, Tensor W2, Tensor offsets,
+                                                   Tensor dOut1, Tensor dOut2) {
+  return {at::empty_like(W1), at::empty_like(X)};
+}
+
+std::tuple<Tensor, Tensor> route_topk(Tensor logits, int64_t k) {
+  return {at::empty({logits.size(0), k}, logits.options()),
+          at::empty({logits.size(0), k}, logits.options().dtype(at::kInt))};
+}
+
+std::tuple<Tensor, Tensor, Tensor> route_topk_count(Tensor logits, int64_t k, Tensor X) {
+  const int64_t T = logits.size(0), E = logits.size(1);
+  const size_t bytes =
+      nt_dispatch_workspace_bytes(T, (int32_t)k, (int32_t)E, X.size(1), dtype_code(X));
+  return {at::empty({T, k}, logits.options()), at::empty({T, k}, logits.options().dtype(at::kInt)),
+          at::empty({(int64_t)std::max<size_t>(bytes, 1)}, X.options().dtype(at::kByte))};
+}
+
+Tensor route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int64_t num_experts) {
+  return at::empty({gates.size(0), num_experts}, gates.options());
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts) {
+  const int64_t T = X.size(0), d = X.size(1), k = w.size(1), A = T * k;
+  auto i32 = X.options().dtype(at::kInt);
+  return {at::empty({num_experts}, i32),       at::empty({num_experts + 1}, i32),
+          at::empty({A, d}, X.options()),      at::empty({A}, i32),
+          at::empty({A}, i32),                 at::empty({A}, X.options().dtype(at::kFloat)),
+          at::empty({T, k}, i32)};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens_counted(
+    Tensor X, Tensor w, Tensor topk, int64_t num_experts, Tensor ws) {
+  return dispatch_tokens(X, w, topk, num_experts);
+}
+
+Tensor combine_inv(Tensor y, Tensor inv, Tensor w, c10::ScalarType out_dtype) {
+  return at::empty({inv.size(0), y.size(1)}, y.options().dtype(out_dtype));
+}
+
+std::tuple<Tensor, Tensor> combine_backward_inv(Tensor y, Tensor inv, Tensor w, Tensor dY) {
+  return {at::empty_like(y), at::empty(w.sizes(), w.options())};
+}
+
+std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv) {
+  return {at::empty({inv.size(0), dpX.size(1)}, dpX.options()),
+          at::empty({inv.size(0), inv.size(1)}, dpw.options())};
+}
+
+}  // namespace meta
+
 }  // namespace
+
+// The op library: torch.ops.nanotitan.<op>. The eight reference ops keep the
+// names and argument orders of csrc/bindings.cpp:59-92 (pack_tokens_kernel
+// mutates its cursor argument, like the reference's atomic cursor); the
+// others are the layer's fused ops. Implementations: the HIP kernels for GPU
+// tensors (CUDA dispatch key, which ROCm builds of torch use for HIP
+// devices), plain C++ for CPU tensors (cpu_ops.cpp), shapes only for Meta.
+TORCH_LIBRARY(nanotitan, m) {
+  m.def("count_expert_kernel(Tensor topk_experts_per_token, Tensor mask, int num_experts, "
+        "int num_topk_experts) -> Tensor");
+  m.def("pack_tokens_kernel(Tensor X, Tensor topk_weights, Tensor topk_experts, "
+        "Tensor(a!) expert_offset_cpy) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("combine_tokens_kernel(Tensor expert_outputs, Tensor packed_tokenId, "
+        "Tensor packed_topk_weights, int num_tokens, int d_model) -> Tensor");
+  m.def("combine_kernel_backward(Tensor expert_outputs, Tensor packed_tokenIds, "
+        "Tensor packed_topk_weights, Tensor residual_stream_grad, int hidden_dim) "
+        "-> (Tensor, Tensor)");
+  m.def("pack_kernel_backward(Tensor packed_X_grad, Tensor packed_topk_weights_grad, "
+        "Tensor packed_tokenId, Tensor packed_expert, Tensor topk_experts) -> (Tensor, Tensor)");
+  m.def("grouped_gemm_kernel(Tensor X, Tensor expert_offset, Tensor weights) -> Tensor");
+  m.def("bwd_grouped_gemm_dW_kernel(Tensor X, Tensor expert_offset, Tensor dOut) -> Tensor");
+  m.def("bwd_grouped_gemm_dX_kernel(Tensor W_gate, Tensor expert_offset, Tensor dOut) -> Tensor");
+  m.def("grouped_gemm_gelu(Tensor X, Tensor expert_offset, Tensor W) -> (Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dX_gelu(Tensor W, Tensor expert_offset, Tensor dOut, Tensor act_grad) "
+        "-> Tensor");
+  m.def("grouped_gemm_swiglu(Tensor X, Tensor expert_offset, Tensor W_gate, Tensor W_val) "
+        "-> (Tensor, Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dX_swiglu(Tensor W, Tensor expert_offset, Tensor dOut, Tensor gate, "
+        "Tensor value) -> (Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dX2(Tensor W1, Tensor W2, Tensor expert_offset, Tensor dOut1, "
+        "Tensor dOut2) -> Tensor");
+  m.def("bwd_grouped_gemm_dW_dX(Tensor X, Tensor W, Tensor expert_offset, Tensor dOut) "
+        "-> (Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dW_dX_gelu(Tensor act, Tensor W, Tensor expert_offset, Tensor dOut, "
+        "Tensor act_grad) -> (Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dW_dX_swiglu(Tensor hidden, Tensor W, Tensor expert_offset, "
+        "Tensor dOut, Tensor gate, Tensor value) -> (Tensor, Tensor, Tensor)");
+  m.def("bwd_grouped_gemm_dW_dX2(Tensor X, Tensor W1, Tensor W2, Tensor expert_offset, "
+        "Tensor dOut1, Tensor dOut2) -> (Tensor, Tensor)");
+  m.def("route_topk(Tensor logits, int top_k) -> (Tensor, Tensor)");
+  m.def("route_topk_count(Tensor logits, int top_k, Tensor X) -> (Tensor, Tensor, Tensor)");
+  m.def("route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int num_experts) -> Tensor");
+  m.def("dispatch_tokens(Tensor X, Tensor topk_weights, Tensor topk_experts, int num_experts) "
+        "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("dispatch_tokens_counted(Tensor X, Tensor topk_weights, Tensor topk_experts, "
+        "int num_experts, Tensor ws) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("pack_tokens_inv(Tensor X, Tensor topk_weights, Tensor topk_experts, "
+        "Tensor(a!) expert_offset_cpy) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("combine_inv(Tensor expert_outputs, Tensor inv, Tensor packed_topk_weights, "
+        "ScalarType out_dtype) -> Tensor");
+  m.def("combine_backward_inv(Tensor expert_outputs, Tensor inv, Tensor packed_topk_weights, "
+        "Tensor grad) -> (Tensor, Tensor)");
+  m.def("pack_backward_inv(Tensor packed_X_grad, Tensor packed_topk_weights_grad, Tensor inv) "
+        "-> (Tensor, Tensor)");
+}
+
+#define NT_IMPL_ALL(m, NS)                                                  \
+  m.impl("count_expert_kernel", &NS count_expert_kernel);                   \
+  m.impl("pack_tokens_kernel", &NS pack_tokens_kernel);                     \
+  m.impl("combine_tokens_kernel", &NS combine_tokens_kernel);               \
+  m.impl("combine_kernel_backward", &NS combine_kernel_backward);           \
+  m.impl("pack_kernel_backward", &NS pack_kernel_backward);                 \
+  m.impl("grouped_gemm_kernel", &NS grouped_gemm_kernel);                   \
+  m.impl("bwd_grouped_gemm_dW_kernel", &NS bwd_grouped_gemm_dW_kernel);     \
+  m.impl("bwd_grouped_gemm_dX_kernel", &NS bwd_grouped_gemm_dX_kernel);     \
+  m.impl("grouped_gemm_gelu", &NS grouped_gemm_gelu);                       \
+  m.impl("bwd_grouped_gemm_dX_gelu", &NS bwd_grouped_gemm_dX_gelu);         \
+  m.impl("grouped_gemm_swiglu", &NS grouped_gemm_swiglu);                   \
+  m.impl("bwd_grouped_gemm_dX_swiglu", &NS bwd_grouped_gemm_dX_swiglu);     \
+  m.impl("bwd_grouped_gemm_dX2", &NS bwd_grouped_gemm_dX2);                 \
+  m.impl("bwd_grouped_gemm_dW_dX", &NS bwd_grouped_gemm_dW_dX);             \
+  m.impl("bwd_grouped_gemm_dW_dX_gelu", &NS bwd_grouped_gemm_dW_dX_gelu);   \
+  m.impl("bwd_grouped_gemm_dW_dX_swiglu", &NS bwd_grouped_gemm_dW_dX_swiglu); \
+  m.impl("bwd_grouped_gemm_dW_dX2", &NS bwd_grouped_gemm_dW_dX2);           \
+  m.impl("route_topk", &NS route_topk);                                     \
+  m.impl("route_topk_count", &NS route_topk_count);                         \
+  m.impl("route_topk_backward", &NS route_topk_backward);                   \
+  m.impl("dispatch_tokens", &NS dispatch_tokens);                           \
+  m.impl("dispatch_tokens_counted", &NS dispatch_tokens_counted);           \
+  m.impl("pack_tokens_inv", &NS pack_tokens_inv);                           \
+  m.impl("combine_inv", &NS combine_inv);                                   \
+  m.impl("combine_backward_inv", &NS combine_backward_inv);                 \
+  m.impl("pack_backward_inv", &NS pack_backward_inv)
+
+TORCH_LIBRARY_IMPL(nanotitan, CUDA, m) { NT_IMPL_ALL(m, ); }
+
+TORCH_LIBRARY_IMPL(nanotitan, Meta, m) { NT_IMPL_ALL(m, meta::); }
+
+#undef NT_IMPL_ALL
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "nanoTitan MoE expert path on MI355X (gfx950): HIP kernels behind the reference op surface";

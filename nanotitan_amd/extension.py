@@ -35,3 +35,11 @@ def get_hip_extension() -> ModuleType:
             "Run `python -m nanotitan_amd.build` before selecting moe_backend='hip'."
         ) from exc
     return _nanotitan_hip
+
+
+def load_op_library():
+    """``torch.ops.nanotitan``: the op library the extension module registers
+    on load (HIP kernels for GPU tensors, C++ kernels for CPU tensors, shape
+    functions for meta tensors). Raises RuntimeError when it is not built."""
+    get_hip_extension()
+    return torch.ops.nanotitan
