@@ -4,25 +4,41 @@ A step is one pass of the hot path over one batch: from router logits,
 fp32 softmax / stable top-k / renorm, fused count + offsets + pack, grouped
 GEMM up with the GELU in its epilogue, grouped GEMM down, combine
 (activation dtype out), then the full backward to dX, dlogits, dW_up and
-dW_down (the GELU backward fused into the down projection's dX GEMM). Inputs are resident in HBM
-before the timed region. Default workload: config C2 (30720 tokens, d=512,
-E=8, top-2, FFN 512->2048->512, bf16), synthetic seeded data, random-init
-weights.
+dW_down (the GELU backward fused into the down projection's dX GEMM). Inputs
+are resident in HBM before the timed region. Headline workload: config C2
+(30720 tokens, d=512, E=8, top-2, FFN 512->2048->512, bf16), synthetic seeded
+data, random-init weights.
 
-Prints ONE JSON line. ``value`` times K steps with only the step's own
-launches on the stream, after W warmup steps launched the same way (the
-GPU's clocks settle over the first ~20 back-to-back steps; the default W
-is past that). ``roofline`` is for the dominant kernel family (the
-grouped GEMMs): algorithmic FLOPs per launch (2*A*K*N) over the average
-launch duration, measured with HIP events on the launch stream around every
-launch in a second timed pass over the same K steps (the event markers
-slow the step by a few percent, so that pass does not feed ``value``). ``cpu_baseline`` times the CPU restatement of the reference
-torch path on a bounded token sample (rank 0, N=1 only).
+Prints ONE JSON line:
 
-Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2] [--ffn gelu|swiglu]
+* ``value``: tokens/s over K timed steps with only the step's own launches
+  on the stream, after W warmup steps launched the same way (the GPU's clocks
+  settle over the first ~20 back-to-back steps; the default W is past that).
+* ``roofline``: the dominant kernel family (the grouped GEMMs): algorithmic
+  FLOPs per launch (2*A*K*N) over the average launch duration, measured with
+  HIP events on the launch stream around every launch in a second timed pass
+  over the same K steps (the event markers slow the step by a few percent, so
+  that pass does not feed ``value``).
+* ``kernels``: the HBM-bound kernels inside those steps (warm: at C2 the
+  working set fits the 256 MB Infinity Cache). ``kernels_cold``: the same
+  kernels standalone, each launch preceded by a full read of a 512 MB scratch
+  buffer outside the events, so their operands come from HBM; median over
+  the repetitions.
+  ``copy_ceiling``: the library's own 16-byte streaming copy under the same
+  cold rule, at about the HBM kernels' sizes, the achievable bandwidth they
+  are measured against.
+* ``configs``: the other BASELINE.json configs (C1, C3, C4, C5) through the
+  same measurement with fewer steps: ms/step, tokens/s, GEMM TF/s and its
+  fraction of the roof, the HBM kernels in the layer and cold.
+* ``cpu_baseline``: the CPU restatement of the reference torch path on the
+  first tokens of the headline inputs (rank 0, N=1 only).
 
-``--ffn swiglu`` runs the reference's SwiGLU ExpertFFN in place of the
-configs' GELU FFN (a secondary figure; the headline is the GELU FFN).
+Headline inputs are drawn on the CPU with a seeded generator and copied to
+the GPU, so the CPU baseline runs on the same bits; the secondary configs are
+drawn on the GPU (no CPU run uses them).
+
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2]
+       [--ffn gelu|swiglu] [--configs all|none|1,3,...]
 """
 
 from __future__ import annotations
@@ -32,6 +48,7 @@ import json
 import math
 import os
 import platform
+import statistics
 import subprocess
 import sys
 import time
@@ -45,6 +62,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = "MoE layer fwd+bwd tokens/sec (1×MI355X); pack/combine HBM GB/s; GEMM MFMA %"
 PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {torch.bfloat16: 2500.0, torch.float16: 2500.0, torch.float32: 157.3}
+# Read between cold timings: twice the Infinity Cache. A read leaves the
+# caches holding clean, unrelated lines; a write would leave dirty lines whose
+# write-back lands inside the next timed kernel (measured: C4 combine 5.0 ->
+# 3.4 TB/s, the 400 MB copy 5.5 -> 3.8 TB/s).
+SCRATCH_BYTES = 512 << 20
 
 # name: (dtype, T, d, E, k, f, weight std, logit std)
 WORKLOADS = {
@@ -54,32 +76,61 @@ WORKLOADS = {
     4: ("C4", torch.bfloat16, 16384, 4096, 8, 2, 14336, 0.01, 1.0),
     5: ("C5", torch.float16, 65536, 2048, 128, 8, 768, 0.02, 2.0),
 }
+SEED = 1234
 
 
-def make_workload(cfg_id: int, device: str, seed: int = 1234, T: int | None = None):
-    """Synthetic inputs of config C<cfg_id>: X, logits (with the config's edits), weights, dY."""
-    name, dtype, T0, d, E, k, f, wstd, lstd = WORKLOADS[cfg_id]
-    T = T0 if T is None else T
-    g = torch.Generator(device=device).manual_seed(seed)
-    X = torch.randn(T, d, generator=g, device=device).to(dtype)
-    logits = torch.randn(T, E, generator=g, device=device) * lstd
+def make_workload(cfg_id: int, device: str, seed: int = SEED, draw: str = "cpu"):
+    """Synthetic inputs of config C<cfg_id>: X, logits (with the config's edits),
+    weights, dY. ``draw="cpu"``: drawn with a CPU generator, then copied to
+    ``device`` (the same bits on every device); ``draw="device"``: drawn on
+    ``device`` directly (faster for the large configs)."""
+    name, dtype, T, d, E, k, f, wstd, lstd = WORKLOADS[cfg_id]
+    gdev = "cpu" if draw == "cpu" else device
+    g = torch.Generator(device=gdev).manual_seed(seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=gdev)
+
+    X = randn(T, d).to(dtype)
+    logits = randn(T, E) * lstd
     if cfg_id == 3:  # Zipf(1.2) expert popularity as a log-prior bias
         z = torch.tensor([(i + 1) ** -1.2 for i in range(E)], dtype=torch.float64)
         perm = torch.randperm(E, generator=torch.Generator().manual_seed(seed))
-        logits += torch.log(z[perm] / z.sum()).float().to(device)
+        logits += torch.log(z[perm] / z.sum()).float().to(gdev)
     if cfg_id == 5:  # 16 dead experts, 1% of tokens with all live logits tied
         cg = torch.Generator().manual_seed(seed)
         dead = torch.randperm(E, generator=cg)[:16]
         ties = torch.randperm(T, generator=cg)[: math.ceil(T / 100)]
         live = torch.ones(E, dtype=torch.bool)
         live[dead] = False
-        logits[ties.to(device).unsqueeze(1), live.nonzero().squeeze(1).to(device).unsqueeze(0)] = 0.0
-        logits[:, dead.to(device)] = float("-inf")
-    W_up = (torch.randn(E, d, f, generator=g, device=device) * wstd).to(dtype)
-    W_down = (torch.randn(E, f, d, generator=g, device=device) * wstd).to(dtype)
-    dY = torch.randn(T, d, generator=g, device=device).to(dtype)
-    return dict(name=name, dtype=dtype, T=T, d=d, E=E, k=k, f=f, X=X, logits=logits,
-                W_up=W_up, W_down=W_down, dY=dY)
+        logits[ties.to(gdev).unsqueeze(1), live.nonzero().squeeze(1).to(gdev).unsqueeze(0)] = 0.0
+        logits[:, dead.to(gdev)] = float("-inf")
+    W_up = (randn(E, d, f) * wstd).to(dtype)
+    W_down = (randn(E, f, d) * wstd).to(dtype)
+    dY = randn(T, d).to(dtype)
+    wl = dict(name=name, dtype=dtype, T=T, d=d, E=E, k=k, f=f, X=X, logits=logits,
+              W_up=W_up, W_down=W_down, dY=dY, seed=seed, draw=draw)
+    for key in ("X", "logits", "W_up", "W_down", "dY"):
+        wl[key] = wl[key].to(device)
+    return wl
+
+
+# Algorithmic bytes of the HBM-bound kernels (each tensor touched once):
+# dispatch reads X, the ids and gates and writes the packed rows, ids and
+# gates; combine reads the packed rows, gates and the inverse map and writes
+# [T,d]; combine backward reads dY once and the packed rows, writes dy and
+# dw; pack backward reads the packed grads, gate grads and inverse map and
+# writes dX and dw.
+def hbm_bytes(kind, T, d, A, b, b_out=None, b_grad=None):
+    if kind == "dispatch":
+        return T * d * b + A * d * b + 8.0 * A + 12.0 * A
+    if kind == "combine_fwd":
+        return A * d * b + 8.0 * A + T * d * (b if b_out is None else b_out)
+    if kind == "combine_bwd":
+        return T * d * (b if b_grad is None else b_grad) + 2.0 * A * d * b + 12.0 * A
+    if kind == "pack_bwd":
+        return A * d * b + T * d * b + 12.0 * A
+    raise ValueError(kind)
 
 
 class LaunchTimer:
@@ -108,7 +159,7 @@ class LaunchTimer:
     def __init__(self, ext):
         self._ext = ext
         self.active = False
-        self.records = []  # (family, name, start_event, end_event, work)
+        self.records = []  # (family, name, start_event, end_event, work, launches)
 
     def __getattr__(self, name):
         fn = getattr(self._ext, name)
@@ -171,28 +222,21 @@ class LaunchTimer:
             X, _W, _off, G = args[:4]
             return 2 * 2.0 * X.shape[0] * X.shape[1] * G.shape[1]
         if name in ("dispatch_tokens", "dispatch_tokens_counted"):
-            # read X once, write packed rows, ids/gates
-            X, w, topk = args[:3]
-            T, d = X.shape
-            A = topk.numel()
-            b = X.element_size()
-            return T * d * b + A * d * b + 8.0 * A + 12.0 * A
-        if name == "combine_inv":  # read packed rows + gates/inv, write [T,d] in out dtype
-            y, inv, w, out_dtype = args
-            A, d = y.shape
-            T = inv.shape[0]
+            X, _w, topk = args[:3]
+            return hbm_bytes("dispatch", X.shape[0], X.shape[1], topk.numel(), X.element_size())
+        if name == "combine_inv":
+            y, inv, _w, out_dtype = args
             ob = torch.empty(0, dtype=out_dtype).element_size()
-            return A * d * y.element_size() + 8.0 * A + T * d * ob
-        if name == "combine_backward_inv":  # read dY once, y; write dy, dw
-            y, inv, w, dY = args
-            A, d = y.shape
-            T = inv.shape[0]
-            return T * d * dY.element_size() + 2.0 * A * d * y.element_size() + 12.0 * A
-        if name == "pack_backward_inv":  # read dpX, dpw, inv; write dX, dw
-            dpX, dpw, inv = args
-            A, d = dpX.shape
-            T = inv.shape[0]
-            return A * d * dpX.element_size() + T * d * dpX.element_size() + 12.0 * A
+            return hbm_bytes("combine_fwd", inv.shape[0], y.shape[1], y.shape[0],
+                             y.element_size(), b_out=ob)
+        if name == "combine_backward_inv":
+            y, inv, _w, dY = args
+            return hbm_bytes("combine_bwd", inv.shape[0], y.shape[1], y.shape[0],
+                             y.element_size(), b_grad=dY.element_size())
+        if name == "pack_backward_inv":
+            dpX, _dpw, inv = args
+            return hbm_bytes("pack_bwd", inv.shape[0], dpX.shape[1], dpX.shape[0],
+                             dpX.element_size())
         return 0.0
 
     def summary(self):
@@ -204,16 +248,6 @@ class LaunchTimer:
             r["ms"] += ms
             r["work"] += work
         return out
-
-
-def gpu_step(wl, W_up, W_down, ffn):
-    from nanotitan_amd.layer import moe_forward_from_logits
-
-    x = wl["X"].detach().requires_grad_(True)
-    logits = wl["logits"].detach().requires_grad_(True)
-    out, _counts, _probs = moe_forward_from_logits(x, logits, ffn, wl["E"], wl["k"])
-    out.backward(wl["dY"])
-    return out
 
 
 class _GeluFFN(torch.nn.Module):
@@ -243,6 +277,150 @@ class _SwiGLUFFN(torch.nn.Module):
         return swiglu_ffn_fn(packed_X, self.W_gate, self.W_val, self.W_out, offsets)
 
 
+def gemm_roof(wl):
+    """Roof of the config's grouped GEMMs: the dense MFMA peak of its dtype,
+    or HBM bandwidth x arithmetic intensity when that is lower (C3). The
+    intensity is the up-projection's 2*A*d*f over (A*d + E*d*f + A*f) bytes."""
+    A, d, f, E = wl["T"] * wl["k"], wl["d"], wl["f"], wl["E"]
+    b = torch.empty(0, dtype=wl["dtype"]).element_size()
+    ai = 2.0 * A * d * f / ((A * d + E * d * f + A * f) * b)
+    peak = PEAK_TFLOPS[wl["dtype"]]
+    hbm_roof = ai * PEAK_HBM_GBS / 1e3
+    return dict(peak_tflops=peak, intensity_flop_per_byte=round(ai, 1),
+                roof_tflops=round(min(peak, hbm_roof), 1),
+                bound="mfma" if peak <= hbm_roof else "hbm")
+
+
+def run_layer(timer, wl, steps, warmup, ffn_kind):
+    """Warmup, then K timed steps without markers, then K steps with HIP
+    events around every launch. Returns the timings and per-family records."""
+    from nanotitan_amd.layer import moe_forward_from_logits
+
+    W_up = wl["W_up"].detach().requires_grad_(True)
+    W_down = wl["W_down"].detach().requires_grad_(True)
+    W_val = None
+    ffn = _GeluFFN(W_up, W_down)
+    if ffn_kind == "swiglu":  # W_up serves as W_gate and W_down as W_out
+        g = torch.Generator(device="cuda").manual_seed(4321)
+        std = WORKLOADS[int(wl["name"][1])][7]
+        W_val = (torch.randn(W_up.shape, generator=g, device="cuda") * std).to(wl["dtype"])
+        W_val.requires_grad_(True)
+        ffn = _SwiGLUFFN(W_up, W_val, W_down)
+
+    def step():
+        x = wl["X"].detach().requires_grad_(True)
+        logits = wl["logits"].detach().requires_grad_(True)
+        out, _counts, _gates = moe_forward_from_logits(x, logits, ffn, wl["E"], wl["k"])
+        out.backward(wl["dY"])
+        W_up.grad = W_down.grad = None
+        if W_val is not None:
+            W_val.grad = None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    timer.records.clear()
+    timer.active = True
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed_events = time.perf_counter() - t1
+    timer.active = False
+    fams = timer.summary()
+    timer.records.clear()
+    return elapsed, elapsed_events, fams
+
+
+def family_report(fams, wl):
+    """GEMM TF/s against the roof, HBM kernels' GB/s against 8 TB/s."""
+    kernels = {}
+    for fam, r in fams.items():
+        avg_ms = r["ms"] / r["launches"]
+        per = r["work"] / r["launches"]
+        if fam == "gemm":
+            roof = gemm_roof(wl)
+            tf = per / avg_ms / 1e9
+            kernels[fam] = {"avg_ms": round(avg_ms, 4), "tflops": round(tf, 2),
+                            "frac_of_peak": round(tf / roof["peak_tflops"], 4),
+                            "frac_of_roof": round(tf / roof["roof_tflops"], 4), **roof}
+        else:
+            gbs = per / (avg_ms * 1e-3) / 1e9
+            kernels[fam] = {"avg_ms": round(avg_ms, 4), "GB_s": round(gbs, 1),
+                            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": per}
+    return kernels
+
+
+def _cold_median(fn, scratch, reps):
+    """Median device time of fn() (HIP events on the current stream), each
+    launch preceded by a full read of `scratch` outside the events."""
+    times = []
+    for _ in range(reps):
+        scratch.sum(dtype=torch.int64)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
+
+
+def cold_hbm_kernels(ext, wl, scratch, reps=10):
+    """The layer's HBM-bound kernels standalone on this config's routing, cold."""
+    T, d, E, k = wl["T"], wl["d"], wl["E"], wl["k"]
+    A = T * k
+    b = torch.empty(0, dtype=wl["dtype"]).element_size()
+    X, dY = wl["X"], wl["dY"]
+    gates, topk = ext.route_topk(wl["logits"].contiguous(), k)
+    _c, _o, packed_X, _tid, _ex, packed_w, inv = ext.dispatch_tokens(X, gates, topk, E)
+    y = packed_X  # expert outputs: any [A,d] rows of the activation dtype
+    cases = {
+        "dispatch": (lambda: ext.dispatch_tokens(X, gates, topk, E),
+                     hbm_bytes("dispatch", T, d, A, b)),
+        "combine_fwd": (lambda: ext.combine_inv(y, inv, packed_w, wl["dtype"]),
+                        hbm_bytes("combine_fwd", T, d, A, b)),
+        "combine_bwd": (lambda: ext.combine_backward_inv(y, inv, packed_w, dY),
+                        hbm_bytes("combine_bwd", T, d, A, b)),
+        "pack_bwd": (lambda: ext.pack_backward_inv(y, packed_w, inv),
+                     hbm_bytes("pack_bwd", T, d, A, b)),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        fn()  # first launch (code object load, allocator) outside the timing
+        ms = _cold_median(fn, scratch, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 1), "GB_s": round(gbs, 1),
+                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes}
+    return out
+
+
+def copy_ceiling(ext, scratch, reps=10):
+    """The library's streaming copy (nt_stream_copy), cold, at about the
+    bytes the C2/C4 and C5 HBM kernels move: GB/s of bytes read + written."""
+    out = {}
+    for label, moved in (("moved_400MB", 400e6), ("moved_2400MB", 2400e6)):
+        n = int(moved // 2) // 16 * 16
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        ext.stream_copy(dst, src)
+        ms = _cold_median(lambda: ext.stream_copy(dst, src), scratch, reps)
+        gbs = 2.0 * n / (ms * 1e-3) / 1e9
+        out[label] = {"us": round(ms * 1e3, 1), "GB_s": round(gbs, 1),
+                      "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+        del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model() -> str:
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
@@ -254,51 +432,95 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(cfg_id: int, budget_s: float = 20.0):
-    """The reference torch CPU path (oracle restatement) on a bounded token sample."""
+def cpu_baseline(wl_cpu, budget_s: float = 20.0):
+    """The reference torch CPU path (oracle restatement) on the first tokens of
+    the same inputs the GPU ran (drawn on the CPU), sized to ~budget_s."""
     from oracle import moe_oracle as O
 
-    name, dtype, T0, d, E, k, f, wstd, lstd = WORKLOADS[cfg_id]
-    cores = os.cpu_count() or 1
-    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
-    torch.set_num_threads(cores)
+    host_cores = os.cpu_count() or 1
+    cap = int(os.environ.get("OMP_NUM_THREADS", host_cores))
+    torch.set_num_threads(max(1, min(host_cores, cap)))
+    k, T0 = wl_cpu["k"], wl_cpu["T"]
+    weights = {"up": wl_cpu["W_up"], "down": wl_cpu["W_down"]}
 
-    def layer(wl):
-        weights = {"up": wl["W_up"], "down": wl["W_down"]}
-        O.moe_layer_torch(wl["X"], wl["logits"], weights, k, ffn="gelu", dY=wl["dY"])
+    def layer(T):
+        O.moe_layer_torch(wl_cpu["X"][:T], wl_cpu["logits"][:T], weights, k, ffn="gelu",
+                          dY=wl_cpu["dY"][:T])
 
     # Size the sample from a 256-token probe so that warmup + timed
     # iterations stay near budget_s (fp16 on the CPU is slow at C5).
     T = min(T0, 256)
-    probe = make_workload(cfg_id, "cpu", seed=99, T=T)
-    layer(probe)
+    layer(T)
     t0 = time.perf_counter()
-    layer(probe)
+    layer(T)
     per_token = (time.perf_counter() - t0) / T
     T = int(min(T0, 4096, max(256, budget_s / 4 / per_token)) // 256 * 256)
     print(f"bench.py: cpu_baseline sample {T} tokens (~{per_token * T:.1f} s per iteration)",
           file=sys.stderr, flush=True)
-    if T == probe["T"]:
-        wl, first = probe, per_token * T  # the probe runs were the warmup
-    else:
-        wl = make_workload(cfg_id, "cpu", seed=99, T=T)
-        t0 = time.perf_counter()
-        layer(wl)  # warmup
-        first = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    layer(T)  # warmup
+    first = time.perf_counter() - t0
     iters = max(1, min(3, int(budget_s / max(first, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(iters):
-        layer(wl)
+        layer(T)
     dt = (time.perf_counter() - t0) / iters
     return {
         "value": T / dt,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "host_cores": host_cores,
+        "thread_cap": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
-        "sample": f"{name} routing and widths, first {T} of {T0} tokens, {dtype}, "
-                  f"1 warmup + {iters} timed fwd+bwd iterations; host CPU: {cpu_model()}; "
+        "sample": f"{wl_cpu['name']} headline inputs (seed {wl_cpu['seed']}, drawn on the CPU, "
+                  f"the same bits the GPU ran): first {T} of {T0} tokens, {wl_cpu['dtype']}, "
+                  f"1 warmup + {iters} timed fwd+bwd iterations on {torch.get_num_threads()} "
+                  f"threads of {host_cores} host cores (thread cap OMP_NUM_THREADS="
+                  f"{os.environ.get('OMP_NUM_THREADS', 'unset')}); host CPU: {cpu_model()}; "
                   f"torch {torch.__version__}",
     }
+
+
+def profile_fields(wl, ffn_kind):
+    """HBM traffic and MFMA busy fraction of the GEMMs from the committed
+    rocprofv3 counter summaries (profiles/*.json), tagged with the commit whose
+    kernels they were measured on."""
+    out = {}
+    if ffn_kind != "gelu":
+        return out
+    prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
+    if prof.exists():
+        js = json.loads(prof.read_text())
+        fams_t = js.get("families", {})
+        # GEMM launches of one step: up (fused GELU), down, and the backward's
+        # down dX (fused GELU backward), up dX and two dW, either as paired
+        # launches (dW + dX in one kernel, two GEMMs each) or one by one;
+        # traffic per GEMM averaged over the six.
+        per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_pair_dw_dx_gelu": 1,
+                    "gemm_pair_dw_dx": 1}
+        if not all(f in fams_t for f in per_step):
+            per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_dx_gelu": 1, "gemm_dx": 1,
+                        "gemm_dw": 2}
+        if all(f in fams_t for f in per_step):
+            n = 6
+            out["traffic"] = round(sum(fams_t[f]["bytes"] * c for f, c in per_step.items()) / n)
+            out["traffic_algorithmic"] = round(
+                sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
+            out["traffic_source"] = f"profiles/{prof.name} (kernels of commit " \
+                                    f"{js.get('commit', 'unrecorded')})"
+    mf = ROOT / "profiles" / f"mfma_{wl['name'].lower()}.json"
+    if mf.exists():
+        js = json.loads(mf.read_text())
+        fam_m = {k: v for k, v in js.items() if isinstance(v, dict)}
+        t_all = sum(v["launches"] * v["avg_us"] for v in fam_m.values())
+        if t_all > 0:
+            def tw(key):
+                return sum(v[key] * v["launches"] * v["avg_us"] for v in fam_m.values()) / t_all
+            out["mfma_busy_frac"] = round(tw("mfma_busy_frac"), 4)
+            out["clock_ghz"] = round(tw("clock_ghz"), 3)
+            out["mfma_source"] = f"profiles/{mf.name} (kernels of commit " \
+                                 f"{js.get('commit', 'unrecorded')})"
+    return out
 
 
 def main():
@@ -307,6 +529,11 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
+    ap.add_argument("--configs", default="all",
+                    help="secondary configs to measure as well: all, none, or ids like 1,3,4")
+    ap.add_argument("--config-steps", type=int, default=20)
+    ap.add_argument("--config-warmup", type=int, default=10)
+    ap.add_argument("--cold-reps", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--ffn", choices=["gelu", "swiglu"], default="gelu",
@@ -315,18 +542,6 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 1 GiB (HBM counter calibration) and exit")
     args = ap.parse_args()
-
-    if args.copy_probe:
-        nbytes = 1 << 30
-        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes,
-                          "launches": 5}), flush=True)
-        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -344,58 +559,29 @@ def main():
     from nanotitan_amd.extension import get_hip_extension
 
     ext = get_hip_extension()
+
+    if args.copy_probe:
+        nbytes = 1 << 30
+        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            ext.stream_copy(dst, src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes,
+                          "launches": 5}), flush=True)
+        return
+
     timer = LaunchTimer(ext)
     moe_ops.get_hip_extension = lambda: timer
 
     torch.manual_seed(0)
-    wl = make_workload(args.config, "cuda")
-    W_up = wl["W_up"].detach().requires_grad_(True)
-    W_down = wl["W_down"].detach().requires_grad_(True)
-    ffn = _GeluFFN(W_up, W_down)
-    W_val = None
-    if args.ffn == "swiglu":  # W_up serves as W_gate and W_down as W_out
-        std = WORKLOADS[args.config][7]
-        g = torch.Generator(device="cuda").manual_seed(4321)
-        W_val = (torch.randn(W_up.shape, generator=g, device="cuda") * std).to(wl["dtype"])
-        W_val.requires_grad_(True)
-        ffn = _SwiGLUFFN(W_up, W_val, W_down)
-
-    for _ in range(args.warmup):
-        gpu_step(wl, W_up, W_down, ffn)
-        W_up.grad = W_down.grad = None
-        if W_val is not None:
-            W_val.grad = None
-    torch.cuda.synchronize()
-
-    # Headline: K steps with nothing but the step's own launches on the stream.
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        gpu_step(wl, W_up, W_down, ffn)
-        W_up.grad = W_down.grad = None
-        if W_val is not None:
-            W_val.grad = None
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-
-    # Per-launch timing: the same K steps again, with a HIP event pair around
-    # every kernel-family launch on the launch stream. The event markers add
-    # a few percent to the step, so this pass does not feed `value`.
-    timer.active = True
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for _ in range(args.steps):
-        gpu_step(wl, W_up, W_down, ffn)
-        W_up.grad = W_down.grad = None
-        if W_val is not None:
-            W_val.grad = None
-    torch.cuda.synchronize()
-    elapsed_events = time.perf_counter() - t1
-    timer.active = False
+    wl_cpu = make_workload(args.config, "cpu", draw="cpu")
+    wl = {k: (v.to("cuda") if isinstance(v, torch.Tensor) else v) for k, v in wl_cpu.items()}
+    elapsed, elapsed_events, fams = run_layer(timer, wl, args.steps, args.warmup, args.ffn)
 
     ms_per_step = elapsed / args.steps * 1e3
     tokens_per_s = wl["T"] * args.steps / elapsed
-    fams = timer.summary()
     gemm = fams.get("gemm", {"launches": 0, "ms": 0.0, "work": 0.0})
     peak = PEAK_TFLOPS[wl["dtype"]]
     achieved = (gemm["work"] / (gemm["ms"] * 1e-3) / 1e12) if gemm["ms"] > 0 else 0.0
@@ -413,51 +599,41 @@ def main():
                   f"({elapsed_events / args.steps * 1e3:.4f} ms/step with the events); a paired "
                   f"dW + dX call counts as two launches over its joint span",
     }
-    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
-    # (calibrated on a device copy), committed with the profile summaries.
-    prof = ROOT / "profiles" / f"traffic_{wl['name'].lower()}.json"
-    if prof.exists() and args.ffn == "gelu":
-        fams_t = json.loads(prof.read_text()).get("families", {})
-        # GEMM launches of one step: up (fused GELU), down, and the backward's
-        # down dX (fused GELU backward), up dX and two dW, either as paired
-        # launches (dW + dX in one kernel, two GEMMs each) or one by one;
-        # traffic per GEMM averaged over the six.
-        per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_pair_dw_dx_gelu": 1,
-                    "gemm_pair_dw_dx": 1}
-        if not all(f in fams_t for f in per_step):
-            per_step = {"gemm_fwd_gelu": 1, "gemm_fwd": 1, "gemm_dx_gelu": 1, "gemm_dx": 1,
-                        "gemm_dw": 2}
-        if all(f in fams_t for f in per_step):
-            n = 6
-            roofline["traffic"] = round(sum(fams_t[f]["bytes"] * c for f, c in per_step.items()) / n)
-            roofline["traffic_algorithmic"] = round(
-                sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
-            roofline["traffic_source"] = f"profiles/{prof.name}"
-    # MFMA busy fraction and running clock of the GEMMs, from a rocprofv3
-    # counter pass (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x 1024
-    # SIMDs) committed with the profile summaries; time-weighted over the
-    # GEMM families of a step.
-    mf = ROOT / "profiles" / f"mfma_{wl['name'].lower()}.json"
-    if mf.exists() and args.ffn == "gelu":
-        fam_m = json.loads(mf.read_text())
-        t_all = sum(v["launches"] * v["avg_us"] for v in fam_m.values())
-        if t_all > 0:
-            def tw(key):
-                return sum(v[key] * v["launches"] * v["avg_us"] for v in fam_m.values()) / t_all
-            roofline["mfma_busy_frac"] = round(tw("mfma_busy_frac"), 4)
-            roofline["clock_ghz"] = round(tw("clock_ghz"), 3)
-            roofline["mfma_source"] = f"profiles/{mf.name}"
-    kernels = {}
-    for fam, r in fams.items():
-        avg_ms = r["ms"] / r["launches"]
-        per = r["work"] / r["launches"]
-        if fam == "gemm":
-            kernels[fam] = {"avg_ms": round(avg_ms, 4), "tflops": round(per / avg_ms / 1e9, 2)}
-        else:
-            gbs = per / (avg_ms * 1e-3) / 1e9
-            kernels[fam] = {"avg_ms": round(avg_ms, 4), "GB_s": round(gbs, 1),
-                            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": per}
+    roofline.update(profile_fields(wl, args.ffn))
+    kernels = family_report(fams, wl)
 
+    scratch = torch.ones(SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
+    kernels_cold = cold_hbm_kernels(ext, wl, scratch, args.cold_reps)
+    ceiling = copy_ceiling(ext, scratch, args.cold_reps)
+    del wl
+    torch.cuda.empty_cache()
+
+    configs = {}
+    if args.configs != "none":
+        ids = sorted(WORKLOADS) if args.configs == "all" else [int(c) for c in args.configs.split(",")]
+        for cid in ids:
+            if cid == args.config:
+                continue
+            w2 = make_workload(cid, "cuda", draw="device")
+            e2, ee2, f2 = run_layer(timer, w2, args.config_steps, args.config_warmup, args.ffn)
+            rep = family_report(f2, w2)
+            configs[w2["name"]] = {
+                "workload": f"{w2['T']} tokens x d={w2['d']}, E={w2['E']}, top-{w2['k']}, "
+                            f"FFN {w2['d']}->{w2['f']}->{w2['d']}, {w2['dtype']}",
+                "tokens_per_s": round(w2["T"] * args.config_steps / e2, 1),
+                "ms_per_step": round(e2 / args.config_steps * 1e3, 4),
+                "steps": args.config_steps,
+                "warmup": args.config_warmup,
+                "gemm": rep.pop("gemm", None),
+                "hbm_in_layer": rep,
+                "hbm_cold": cold_hbm_kernels(ext, w2, scratch, args.cold_reps),
+            }
+            del w2
+            torch.cuda.empty_cache()
+    del scratch
+    torch.cuda.empty_cache()
+
+    name, dtype_, T, d, E, k, f, _ws, _ls = WORKLOADS[args.config]
     result = {
         "metric": METRIC,
         "value": round(tokens_per_s, 1),
@@ -469,25 +645,29 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[wl["dtype"]],
-        "data": "synthetic (seeded N(0,1) activations/logits, N(0,std^2) random-init expert weights)",
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype_],
+        "data": "synthetic (seeded N(0,1) activations/logits, N(0,std^2) random-init expert "
+                "weights; headline drawn on the CPU)",
         "config": {
-            "workload": f"{wl['name']}: MoE layer fwd+bwd, {wl['T']} tokens x d={wl['d']}, "
-                        f"E={wl['E']}, top-{wl['k']}, FFN {wl['d']}->{wl['f']}->{wl['d']} "
+            "workload": f"{name}: MoE layer fwd+bwd, {T} tokens x d={d}, E={E}, top-{k}, "
+                        f"FFN {d}->{f}->{d} "
                         + ("GELU" if args.ffn == "gelu" else "SwiGLU (reference ExpertFFN)"),
-            "tokens": wl["T"],
-            "d_model": wl["d"],
-            "num_experts": wl["E"],
-            "top_k": wl["k"],
-            "ffn": wl["f"],
+            "tokens": T,
+            "d_model": d,
+            "num_experts": E,
+            "top_k": k,
+            "ffn": f,
             "parallelism": "single-gpu",
         },
         "roofline": roofline,
         "kernels": kernels,
+        "kernels_cold": kernels_cold,
+        "copy_ceiling": ceiling,
+        "configs": configs,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(wl_cpu, args.cpu_budget)
     print(json.dumps(result), flush=True)
 
 

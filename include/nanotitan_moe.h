@@ -68,6 +68,14 @@ const char* nt_strerror(int code);
 /* Library version, major*10000 + minor*100 + patch. */
 int nt_version(void);
 
+/* dst[0..bytes) = src[0..bytes) with 16-byte vector loads (non-temporal) and
+ * stores, four in flight per lane, on `blocks` workgroups of 256 lanes
+ * (0: 8192). The
+ * achievable-bandwidth reference the HBM-bound kernels are measured against:
+ * a copy moves 2 * bytes. Replaces the reference's copy_kernel_vector
+ * (csrc/kernels/copy_kernel.cu:25-36, benchmarks/mem_copy_benchmark.py:52-95). */
+int nt_stream_copy(void* dst, const void* src, size_t bytes, int32_t blocks, hipStream_t stream);
+
 /* ------------------------------------------------------------------ dispatch */
 
 /* Workspace for nt_count_experts / nt_pack_tokens / nt_dispatch with these

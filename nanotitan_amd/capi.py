@@ -31,6 +31,7 @@ _P = c_void_p  # any device pointer, hipStream_t included
 EXPORTS: dict[str, tuple[object, list[object]]] = {
     "nt_strerror": (c_char_p, [c_int]),
     "nt_version": (c_int, []),
+    "nt_stream_copy": (c_int, [_P, _P, c_size_t, c_int32, _P]),
     "nt_dispatch_workspace_bytes": (c_size_t, [c_int64, c_int32, c_int32, c_int64, c_int]),
     "nt_count_experts": (
         c_int,

@@ -35,11 +35,15 @@ struct alignas(sizeof(S) * N) vpack {
   S v[N];
 };
 
-// VE consecutive elements of type T, as floats.
+// VE consecutive elements of type T, as floats. Every row these kernels read
+// (packed rows, gradient rows) is read once: the load is non-temporal, so it
+// does not displace lines other waves still need.
 template <typename T, int VE>
 __device__ __forceinline__ void load_vec(const typename elem<T>::storage* p, float (&out)[VE]) {
   using S = typename elem<T>::storage;
-  const vpack<S, VE> v = *reinterpret_cast<const vpack<S, VE>*>(p);
+  using W = typename nt_word<sizeof(S) * VE>::type;
+  const vpack<S, VE> v =
+      __builtin_bit_cast(vpack<S, VE>, __builtin_nontemporal_load(reinterpret_cast<const W*>(p)));
 #pragma unroll
   for (int i = 0; i < VE; ++i) out[i] = elem<T>::load(v.v[i]);
 }

@@ -81,6 +81,48 @@ inline int dtype_bytes(int dtype) {
   }
 }
 
+// Integer or integer-vector type of B bytes, for __builtin_nontemporal_load
+// of B-byte chunks (the builtin takes scalar and vector types only).
+template <int B>
+struct nt_word;
+// 32 and 64 bytes: instantiated by vector-width switches for wide element
+// types, never selected at run time (16-byte accesses at most).
+template <>
+struct nt_word<64> {
+  typedef uint32_t type __attribute__((ext_vector_type(16)));
+};
+template <>
+struct nt_word<32> {
+  typedef uint32_t type __attribute__((ext_vector_type(8)));
+};
+template <>
+struct nt_word<16> {
+  typedef uint32_t type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct nt_word<8> {
+  typedef uint32_t type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct nt_word<4> {
+  typedef uint32_t type;
+};
+template <>
+struct nt_word<2> {
+  typedef uint16_t type;
+};
+template <>
+struct nt_word<1> {
+  typedef uint8_t type;
+};
+
+// Non-temporal load of one V (any trivially copyable 1/2/4/8/16-byte type).
+template <typename V>
+__device__ __forceinline__ V load_nt(const V* p) {
+  using W = typename nt_word<sizeof(V)>::type;
+  return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const W*>(p)));
+}
+
 // ------------------------------------------------------------ wave64 helpers
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -103,7 +103,7 @@ __device__ __forceinline__ void copy_row_to_slots(const V* __restrict__ src, V* 
                                                   int64_t nv, const int32_t* slots, int k) {
   const int lane = lane_id();
   for (int64_t c = lane; c < nv; c += kWave) {
-    const V v = src[c];
+    const V v = load_nt(src + c);  // each token row is read once
     for (int j = 0; j < k; ++j) {
       const int32_t p = slots[j];
       if (p >= 0) dst[(int64_t)p * nv + c] = v;
@@ -185,7 +185,7 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
 #pragma unroll
     for (int u = 0; u < kRowBatch; ++u) {
       const int tt = wave + u * kDispatchWaves;
-      if (on && tt < ntok) pre[u] = src[(tok0 + tt) * nv + lane];
+      if (on && tt < ntok) pre[u] = load_nt(src + (tok0 + tt) * nv + lane);
     }
   }
 
@@ -233,7 +233,7 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
         for (int u = 0; u < kRowBatch; ++u) {
           const int tt = t + u * kDispatchWaves;
           if (t == wave) v[u] = pre[u];
-          else if (on && tt < ntok) v[u] = src[(tok0 + tt) * nv + lane];
+          else if (on && tt < ntok) v[u] = load_nt(src + (tok0 + tt) * nv + lane);
         }
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u) {

@@ -1,7 +1,74 @@
-// Library-wide entry points: status messages and version.
+// Library-wide entry points: status messages, version, and the streaming
+// copy that measures the achievable HBM bandwidth the HBM-bound kernels are
+// graded against.
+#include <algorithm>
+
 #include "common.hpp"
 
+namespace nt {
+namespace {
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 4;  // 16-byte vectors in flight per lane
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// dst[i] = src[i] over n 16-byte vectors: each workgroup moves contiguous
+// runs of kCopyThreads * kCopyUnroll vectors (all loads issued before the
+// stores), grid-striding over the runs. The loads are non-temporal (the
+// source is read once: it need not displace other lines from the caches).
+// Measured cold on MI355X against plain loads, 2/8 vectors per lane and
+// non-temporal stores: this form with 8192 workgroups moves 400 MB at
+// 6.4 TB/s and 2.4 GB at 6.2 TB/s.
+__global__ void __launch_bounds__(kCopyThreads)
+stream_copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
+  constexpr int64_t kRun = (int64_t)kCopyThreads * kCopyUnroll;
+  for (int64_t base = (int64_t)blockIdx.x * kRun; base < n; base += (int64_t)gridDim.x * kRun) {
+    u32x4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = base + u * kCopyThreads + threadIdx.x;
+      if (i < n) v[u] = __builtin_nontemporal_load(src + i);
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = base + u * kCopyThreads + threadIdx.x;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
+
+__global__ void byte_copy_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                 int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+}  // namespace
+}  // namespace nt
+
 extern "C" {
+
+int nt_stream_copy(void* dst, const void* src, size_t bytes, int32_t blocks, hipStream_t stream) {
+  if (bytes == 0) return NT_OK;
+  if (dst == nullptr || src == nullptr || blocks < 0) return NT_ERR_INVALID_ARG;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src);
+  const int64_t n16 = al % 16 == 0 ? (int64_t)(bytes / 16) : 0;
+  const int64_t runs = nt::ceil_div(n16, (int64_t)nt::kCopyThreads * nt::kCopyUnroll);
+  const int64_t grid = blocks > 0 ? blocks : 8192;  // 32 per CU: enough bytes in flight
+  if (n16 > 0)
+    hipLaunchKernelGGL(nt::stream_copy_kernel, dim3((unsigned)std::min<int64_t>(runs, grid)),
+                       dim3(nt::kCopyThreads), 0, stream, static_cast<const nt::u32x4*>(src),
+                       static_cast<nt::u32x4*>(dst), n16);
+  const int64_t tail = (int64_t)bytes - n16 * 16;
+  if (tail > 0)
+    hipLaunchKernelGGL(nt::byte_copy_kernel,
+                       dim3((unsigned)std::min<int64_t>(nt::ceil_div(tail, 256), 4096)), dim3(256),
+                       0, stream, static_cast<const uint8_t*>(src) + n16 * 16,
+                       static_cast<uint8_t*>(dst) + n16 * 16, tail);
+  return nt::launch_status();
+}
 
 const char* nt_strerror(int code) {
   switch (code) {

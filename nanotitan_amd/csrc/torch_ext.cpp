@@ -720,6 +720,21 @@ std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv)
   return {dX, dw};
 }
 
+// stream_copy(dst, src, blocks=0): the library's 16-byte streaming copy of
+// src's bytes into dst (the achievable-bandwidth reference of the benchmark).
+void stream_copy(Tensor dst, Tensor src, int64_t blocks) {
+  check_device(dst, "dst");
+  check_device(src, "src");
+  TORCH_CHECK(dst.is_contiguous() && src.is_contiguous(), "tensors must be contiguous");
+  const size_t bytes = (size_t)src.numel() * src.element_size();
+  TORCH_CHECK((size_t)dst.numel() * dst.element_size() >= bytes, "dst is smaller than src");
+  check_same_device(dst, {&src});
+  c10::hip::HIPGuard guard(src.get_device());
+  check_status(nt_stream_copy(dst.data_ptr(), src.data_ptr(), bytes, (int32_t)blocks,
+                              stream_of(src)),
+               "stream_copy");
+}
+
 // ------------------------------------------------------------ Meta kernels
 //
 // Output shapes and dtypes only (fake / meta tensors, torch.compile tracing):
@@ -1000,5 +1015,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dispatch_tokens_counted", &dispatch_tokens_counted,
         "dispatch_tokens from the counts route_topk_count computed");
   m.def("route_topk_backward", &route_topk_backward, "Gradient of route_topk's gates -> dlogits");
+  m.def("stream_copy", &stream_copy, "16-byte streaming device copy (bandwidth reference)",
+        pybind11::arg("dst"), pybind11::arg("src"), pybind11::arg("blocks") = 0);
   m.def("version", []() { return nt_version(); });
 }

@@ -72,7 +72,8 @@ def _sample_tokens(idx, logits, E, seed, n=32):
 
 
 @pytest.mark.parametrize("cfg_id,ffn", [(1, "gelu"), (2, "gelu"), (3, "gelu"), (4, "gelu"),
-                                        (5, "gelu"), (2, "swiglu"), (4, "swiglu")])
+                                        (5, "gelu"), (2, "swiglu"), (3, "swiglu"), (4, "swiglu"),
+                                        (5, "swiglu")])
 def test_layer_full_size_sampled_tokens(ext, cfg_id, ffn):
     """The layer forward + backward at the config's full token count (the
     benchmark's path: router with fused count, dispatch, fused expert FFN,
@@ -216,3 +217,63 @@ class _Rows:
 
     def __getitem__(self, rows):
         return self.data[[self.pos[r] for r in rows]]
+
+
+def _boundary_ties(logits, k):
+    """C5's second tie variant: each row's (k+1)-th largest logit is set to
+    its k-th largest (where that is finite), so the top-k boundary is a tie
+    that only the lower-expert-id rule resolves."""
+    z = logits.clone()
+    order = torch.sort(z, dim=1, descending=True, stable=True).indices
+    kth = z.gather(1, order[:, k - 1:k])
+    ok = torch.isfinite(kth).squeeze(1)
+    rows = ok.nonzero().squeeze(1)
+    z[rows, order[rows, k]] = kth[rows, 0]
+    return z
+
+
+def test_c5_boundary_ties_full_size_bit_exact_and_repeatable(ext):
+    """C5 at full size with the boundary-tie variant: top-k indices bit-exact
+    against the stable sort (ties to the lower id) over all 65536 tokens, the
+    layer's output and gradients bit-identical across two runs, and the output
+    equal to the oracle's torch path on sampled tokens."""
+    from nanotitan_amd.layer import moe_forward_from_logits
+    from nanotitan_amd.moe_ops import grouped_gelu_ffn_fn, route_fn
+
+    d = O.make_inputs(5, with_weights=False)
+    c = d["cfg"]
+    logits = _boundary_ties(d["logits"], c.k)
+    order = torch.sort(logits, dim=1, descending=True, stable=True).indices
+    assert bool((logits.gather(1, order[:, c.k - 1:c.k]) == logits.gather(1, order[:, c.k:c.k + 1]))
+                .all())
+    _, want_idx, _ = O.route(logits, c.k)
+    _, idx = route_fn(logits.cuda(), c.k)
+    assert torch.equal(idx.cpu(), want_idx)
+
+    W = _cuda_weights(c, 7105)
+
+    class FFN(torch.nn.Module):
+        def forward(self, px, off):
+            return grouped_gelu_ffn_fn(px, W[0], W[1], off)
+
+    runs = []
+    for _ in range(2):
+        x = d["X"].to(c.dtype).cuda().requires_grad_(True)
+        lg = logits.cuda().requires_grad_(True)
+        out, counts, _ = moe_forward_from_logits(x, lg, FFN(), c.E, c.k)
+        out.backward(d["dY"].to(c.dtype).cuda())
+        torch.cuda.synchronize()
+        runs.append((out.detach().view(torch.int16).cpu(), x.grad.view(torch.int16).cpu(),
+                     lg.grad.cpu(), counts.cpu()))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    assert runs[0][3].long().tolist() == O.count_experts(want_idx, None, c.E).tolist()
+
+    S = _sample_tokens(want_idx, logits, c.E, seed=55)
+    weights = {"up": W[0].cpu(), "down": W[1].cpu()}
+    ref_out, ref = O.moe_layer_torch(d["X"][S].to(c.dtype), logits[S], weights, c.k, ffn="gelu",
+                                     dY=d["dY"][S].to(c.dtype))
+    out16 = runs[0][0].view(c.dtype)
+    torch.testing.assert_close(out16[S].float(), ref_out.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(runs[0][1].view(c.dtype)[S].float(), ref["x"].float(), rtol=2e-2,
+                               atol=2e-2)
