@@ -19,7 +19,7 @@
 // expert. fp32 / fp64 and shapes that are not multiples of 8 run on a simple
 // LDS-tiled FMA kernel with the same scheduler.
 #include <algorithm>
-
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1532,18 +1532,20 @@ bool mfma_ok(int dtype, int64_t K, int64_t N, const void* p0, const void* p1, co
 }
 
 // Compute units of the current device (cached per device id).
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+// CUs of the device that `s` launches on (the null stream: the current
+// device). Concurrent first calls may both query; they store the same value.
+int device_cus(hipStream_t s) {
+  static std::atomic<int> cache[64];
+  hipDevice_t dev = 0;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Tile bookkeeping shared by the launchers: n-tiles, m-tile slots and the
@@ -1583,7 +1585,7 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   // Occupancy of this instantiation (bf16 and fp16 share resource usage).
   static const int per_cu = blocks_per_cu(kb, threads);
   // Persistent: at most one resident wave of workgroups; each walks tiles.
-  const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus() * per_cu);
+  const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus(s) * per_cu);
   const dim3 grid((unsigned)nblocks);
   if (dtype == NT_BF16)
     hipLaunchKernelGGL(kb, grid, dim3(threads), 0, s, g);
@@ -1611,7 +1613,7 @@ int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
     (void)tiles256;
     return launch_mfma<MODE, EPI, 256, 256, 4, 2, 64, 2>(dtype, g, out_cols, s);
   } else {
-    if (tiles256 * 2 >= (int64_t)device_cus() * 3) {
+    if (tiles256 * 2 >= (int64_t)device_cus(s) * 3) {
       if constexpr (MODE != kDw && (EPI == kEpiPlain || EPI == kEpiDualK)) {
         const int64_t red = MODE == kFwd ? g.K : (EPI == kEpiDualK ? 2 * g.N : g.N);
         if (red >= kSplitMinRed)
@@ -1649,7 +1651,7 @@ __global__ void __launch_bounds__(256) gelu_elementwise_kernel(void* io_, void* 
 template <bool GRAD>
 int launch_gelu_elementwise(int dtype, void* io, void* g, int64_t n, hipStream_t s) {
   if (n == 0) return NT_OK;
-  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus() * 16));
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus(s) * 16));
   switch (dtype) {
     case NT_F32: hipLaunchKernelGGL((gelu_elementwise_kernel<float, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
     case NT_F64: hipLaunchKernelGGL((gelu_elementwise_kernel<double, GRAD>), grid, dim3(256), 0, s, io, g, n); break;
@@ -1693,7 +1695,7 @@ template <bool GRAD>
 int launch_swiglu_elementwise(int dtype, void* io, void* dg, const void* g, const void* v,
                               int64_t n, hipStream_t s) {
   if (n == 0) return NT_OK;
-  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus() * 16));
+  const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, 256), (int64_t)device_cus(s) * 16));
   switch (dtype) {
     case NT_F32: hipLaunchKernelGGL((swiglu_elementwise_kernel<float, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
     case NT_F64: hipLaunchKernelGGL((swiglu_elementwise_kernel<double, GRAD>), grid, dim3(256), 0, s, io, dg, g, v, n); break;
@@ -1794,6 +1796,10 @@ int32_t dw_chunk_rows(int64_t A, int64_t K, int64_t N, int32_t E) {
 // than a share: with skewed routing (C3: the head expert has 8x the mean
 // rows) one whole-expert tile would otherwise outlast everything else.
 // Balanced routing stays unsplit.
+// The split is planned for MI355X's 256 CUs on every device: it fixes the
+// summation order, so dW bits and the workspace size do not depend on the
+// device that runs the launch.
+constexpr int64_t kDwSplitCus = 256;
 struct DwSplit {
   int32_t R = 0;    // rows per chunk of a split expert (0: no split)
   int32_t thr = 0;  // experts with more rows than this are split
@@ -1802,7 +1808,7 @@ DwSplit dw_split(int64_t A, int64_t K, int64_t N, int32_t E) {
   DwSplit p;
   const int64_t slab = K * N * 4;
   if (A <= 0 || slab <= 0 || E <= 0 || slab >= kDwBudget) return p;
-  const int64_t W = ceil_div(A * ceil_div(K, 128) * ceil_div(N, 128), 2 * device_cus());
+  const int64_t W = ceil_div(A * ceil_div(K, 128) * ceil_div(N, 128), 2 * kDwSplitCus);
   int64_t R = std::max<int64_t>(ceil_div(W, 2), 1024);
   R = round_up(std::max<int64_t>(R, ceil_div(2 * A * slab, kDwBudget)), 64);
   const int64_t thr = std::max<int64_t>(round_up(ceil_div(5 * W, 4), 64), R);
@@ -1822,10 +1828,10 @@ int64_t dw_slabs(int64_t A, DwSplit p) {
 // Tile shape of a dW launch (not paired): 256x256 tiles when the experts'
 // tiles (with dw_chunk_rows chunks) give at least 1.5 per CU, else 128x128
 // tiles, two workgroups per CU (the rule launch_mfma_auto applies).
-bool dw_big_tiles(int64_t A, int64_t K, int64_t N, int32_t E) {
+bool dw_big_tiles(int64_t A, int64_t K, int64_t N, int32_t E, hipStream_t s) {
   const int32_t R0 = dw_chunk_rows(A, K, N, E);
   const int64_t chunks = R0 > 0 ? E + A / R0 : E;
-  return chunks * ceil_div(K, 256) * ceil_div(N, 256) * 2 >= device_cus() * 3;
+  return chunks * ceil_div(K, 256) * ceil_div(N, 256) * 2 >= device_cus(s) * 3;
 }
 
 // Workspace of the dW entry points: kCtrBytes of tile counters (paired
@@ -1965,7 +1971,7 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
     g.slab_cap = (int32_t)dw_slabs(A, sp);
     g.partial = partial;
   }
-  const int st = dw_big_tiles(A, K, N, E)
+  const int st = dw_big_tiles(A, K, N, E, stream)
                      ? launch_mfma<kDw, kEpiPlain, 256, 256, 2, 4, 64, 2>(dtype, g, N, stream)
                      : launch_mfma<kDw, kEpiPlain, 128, 128, 2, 2, 64, 2>(dtype, g, N, stream);
   if (st != NT_OK || !split) return st;
@@ -1988,7 +1994,7 @@ template <int EPIX>
 int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOut, int32_t E,
                int64_t A, int64_t K, int64_t N, void* dW, void* ws, size_t ws_bytes,
                GemmArgs gx, bool dx_mfma, hipStream_t stream) {
-  const int64_t cus = device_cus();
+  const int64_t cus = device_cus(stream);
   const bool mfma_dw = mfma_ok(dtype, K, N, X, dOut, dW);
   const DwSplit sp = mfma_dw ? dw_split(A, K, N, E) : DwSplit();
   const bool aligned = ws != nullptr && reinterpret_cast<uintptr_t>(ws) % 16 == 0;
