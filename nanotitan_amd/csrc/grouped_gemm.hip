@@ -168,6 +168,7 @@ __device__ bool map_m_tile(const int32_t* __restrict__ offsets, int E, int64_t A
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
@@ -461,33 +462,36 @@ __device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int
   nt = (int)(rem / gsz);
 }
 
-// Operand pointers, strides and valid extents of one output tile.
-struct TileJob {
-  const uint16_t* pa;  // A operand origin (tile rows, reduction 0)
-  const uint16_t* pb;  // B operand origin (tile columns, reduction 0)
+// Operand pointers, strides and valid extents of one output tile, for
+// elements of storage type U (uint16_t: bf16 / fp16; float).
+template <typename U>
+struct TileJobT {
+  const U* pa;  // A operand origin (tile rows, reduction 0)
+  const U* pb;  // B operand origin (tile columns, reduction 0)
   int64_t lda, ldb;
   int64_t rows_valid, cols_valid;  // output rows / columns from the tile origin
   int64_t kred;                    // reduction length
-  uint16_t* po;
+  U* po;
   int64_t ldo;
-  uint16_t* po2;          // second output (GELU: gelu'(h); SwiGLU: gate / dvalue)
-  uint16_t* po3;          // SwiGLU forward: value output
-  const uint16_t* paux;   // GELU backward: gelu'(h); SwiGLU backward: gate
-  const uint16_t* paux2;  // SwiGLU backward: value
-  const uint16_t* pa2;    // two-part dX: second A operand origin
-  const uint16_t* pb2;    // SwiGLU forward: value weights; two-part dX: second W
-  int64_t kred1;          // two-part dX: reduction length of the first part
-  float* pf;              // dW of a split expert: fp32 partial slab origin (or null)
+  U* po2;          // second output (GELU: gelu'(h); SwiGLU: gate / dvalue)
+  U* po3;          // SwiGLU forward: value output
+  const U* paux;   // GELU backward: gelu'(h); SwiGLU backward: gate
+  const U* paux2;  // SwiGLU backward: value
+  const U* pa2;    // two-part dX: second A operand origin
+  const U* pb2;    // SwiGLU forward: value weights; two-part dX: second W
+  int64_t kred1;   // two-part dX: reduction length of the first part
+  float* pf;       // dW of a split expert: fp32 partial slab origin (or null)
 };
+typedef TileJobT<uint16_t> TileJob;
 
 // Operands and extents of logical output tile `logical` (< mtiles * ntn).
 // For the row-tiled modes s_pref must hold the m-tile prefix of the experts
 // (build_m_prefix) and `mtiles` its total.
 // SwiGLU forward tiles are BN wide in the MFMA (gate and value halves) and
 // BN / 2 wide in the output.
-template <int MODE, int BM, int BN, int EPI = kEpiPlain>
+template <int MODE, int BM, int BN, int EPI = kEpiPlain, typename U = uint16_t>
 __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pref, int64_t mtiles,
-                                          int64_t logical, TileJob& j) {
+                                          int64_t logical, TileJobT<U>& j) {
   j.po2 = nullptr;
   j.po3 = nullptr;
   j.paux = nullptr;
@@ -519,14 +523,14 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
       c1 = c0 + g.chunk < r1 ? c0 + g.chunk : r1;
     }
     j.kred = c1 - c0;
-    j.pa = static_cast<const uint16_t*>(g.a) + c0 * g.K + (int64_t)mtl * BM;
+    j.pa = static_cast<const U*>(g.a) + c0 * g.K + (int64_t)mtl * BM;
     j.lda = g.K;
-    j.pb = static_cast<const uint16_t*>(g.b) + c0 * g.N + (int64_t)nt * BN;
+    j.pb = static_cast<const U*>(g.b) + c0 * g.N + (int64_t)nt * BN;
     j.ldb = g.N;
     j.rows_valid = g.K - (int64_t)mtl * BM;
     j.cols_valid = g.N - (int64_t)nt * BN;
     const int64_t tile_off = (int64_t)mtl * BM * g.N + (int64_t)nt * BN;
-    j.po = static_cast<uint16_t*>(g.out) + (int64_t)e * g.K * g.N + tile_off;
+    j.po = static_cast<U*>(g.out) + (int64_t)e * g.K * g.N + tile_off;
     j.ldo = g.N;
     if (nch >= 2) j.pf = g.partial + (int64_t)(s_split[e] + c) * g.K * g.N + tile_off;
   } else {
@@ -543,37 +547,37 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
       constexpr int64_t BNO = EPI == kEpiSwiGLU ? BN / 2 : BN;  // output columns per tile
       const int64_t wofs = (int64_t)e * g.K * g.N + (int64_t)nt * BNO;
       const int64_t oofs = row0 * g.N + (int64_t)nt * BNO;
-      j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.K;
+      j.pa = static_cast<const U*>(g.a) + row0 * g.K;
       j.lda = g.K;
-      j.pb = static_cast<const uint16_t*>(g.b) + wofs;
+      j.pb = static_cast<const U*>(g.b) + wofs;
       j.ldb = g.N;
       j.cols_valid = g.N - (int64_t)nt * BNO;
       j.kred = g.K;
-      j.po = static_cast<uint16_t*>(g.out) + oofs;
+      j.po = static_cast<U*>(g.out) + oofs;
       j.ldo = g.N;
-      if (g.out2) j.po2 = static_cast<uint16_t*>(g.out2) + oofs;
+      if (g.out2) j.po2 = static_cast<U*>(g.out2) + oofs;
       if (EPI == kEpiSwiGLU) {
-        j.pb2 = static_cast<const uint16_t*>(g.b2) + wofs;
-        j.po3 = static_cast<uint16_t*>(g.out3) + oofs;
+        j.pb2 = static_cast<const U*>(g.b2) + wofs;
+        j.po3 = static_cast<U*>(g.out3) + oofs;
       }
     } else {  // kDx
       const int64_t oofs = row0 * g.K + (int64_t)nt * BN;
-      j.pa = static_cast<const uint16_t*>(g.a) + row0 * g.N;
+      j.pa = static_cast<const U*>(g.a) + row0 * g.N;
       j.lda = g.N;
-      j.pb = static_cast<const uint16_t*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
+      j.pb = static_cast<const U*>(g.b) + (int64_t)e * g.K * g.N + (int64_t)nt * BN * g.N;
       j.ldb = g.N;
       j.cols_valid = g.K - (int64_t)nt * BN;
       j.kred = g.N;
-      j.po = static_cast<uint16_t*>(g.out) + oofs;
+      j.po = static_cast<U*>(g.out) + oofs;
       j.ldo = g.K;
-      if (g.aux) j.paux = static_cast<const uint16_t*>(g.aux) + oofs;
+      if (g.aux) j.paux = static_cast<const U*>(g.aux) + oofs;
       if (EPI == kEpiSwiGLUGrad) {
-        j.paux2 = static_cast<const uint16_t*>(g.aux2) + oofs;
-        j.po2 = static_cast<uint16_t*>(g.out2) + oofs;
+        j.paux2 = static_cast<const U*>(g.aux2) + oofs;
+        j.po2 = static_cast<U*>(g.out2) + oofs;
       }
       if (EPI == kEpiDualK) {
-        j.pa2 = static_cast<const uint16_t*>(g.a2) + row0 * g.N;
-        j.pb2 = static_cast<const uint16_t*>(g.b2) + (int64_t)e * g.K * g.N +
+        j.pa2 = static_cast<const U*>(g.a2) + row0 * g.N;
+        j.pb2 = static_cast<const U*>(g.b2) + (int64_t)e * g.K * g.N +
                 (int64_t)nt * BN * g.N;
         j.kred1 = g.N;
         j.kred = 2 * g.N;
@@ -1421,6 +1425,230 @@ __device__ __forceinline__ double from_acc<double>(double v) {
   return v;
 }
 
+// ------------------------------------------------------ fp32 MFMA GEMM
+// fp32 operands on v_mfma_f32_32x32x2_f32 (64 MACs per lane, 2048 per
+// instruction). Tiles of 128x128 outputs, 32-deep k-steps, 4 waves of
+// 64x64 (2x2 MFMA tiles each), two workgroups per CU (2 x 32 KiB LDS
+// stages each). The same tile scheduler and operand roles as the bf16/fp16
+// kernel; direct-to-LDS 16-byte loads, a two-stage ring.
+//
+// Reduction order inside a k-step: lanes 0..31 (the MFMA's k-slot 0) take
+// k = 0..15 of the step and lanes 32..63 (k-slot 1) k = 16..31; MFMA j
+// adds the products of k = j and k = 16 + j. A lane's 16 k values of one
+// row are then contiguous, so a K-major operand is read from LDS as four
+// 16-byte reads per row.
+//
+// LDS layouts (16-byte chunks XOR-swizzled so that every fragment read is
+// conflict-free):
+//   K-major (reduction contiguous in memory): row r (of 128) = 32 floats =
+//     8 chunks, chunk c at position c ^ ((r >> 1) & 7); read 16 bytes a lane.
+//   MN-major: k-row k (of 32) = 128 floats = 32 chunks, chunk c at position
+//     c ^ (8 * (k >> 4)); read 4 bytes a lane (the two half-waves read
+//     k-rows 16 apart, which the swizzle puts in opposite bank halves).
+constexpr int kF32BM = 128, kF32BN = 128, kF32BK = 32, kF32Waves = 4;
+
+template <bool KMAJ>
+struct F32Tile {
+  static constexpr int kBytes = 128 * kF32BK * 4;       // 16 KiB
+  static constexpr int kPer = kBytes / 1024 / kF32Waves;  // load instructions per wave
+  uint32_t off;    // instruction 0: this lane's byte offset from the k-step origin
+  uint32_t ustep;  // byte step between this wave's instructions
+  uint32_t kofs;   // K-major: k of this lane's chunk within the step
+  int wave;
+  // K-major: instruction i = 4u + w covers rows 8i .. 8i+7 (rows 32u + 8w +
+  // lane/8: the swizzle does not depend on u). MN-major: instruction i = 4w
+  // + u covers k-rows 2i, 2i+1 (k-rows 8w + 2u + lane/32: the swizzle does
+  // not depend on u).
+  __device__ void init(int64_t ld, int wave_, int lane) {
+    wave = wave_;
+    if (KMAJ) {
+      const int r = 8 * wave + lane / 8;
+      const int c = (lane % 8) ^ ((r >> 1) & 7);
+      off = (uint32_t)((int64_t)r * ld * 4 + c * 16);
+      ustep = (uint32_t)(32 * ld * 4);
+      kofs = (uint32_t)(4 * c);
+    } else {
+      const int k = 8 * wave + lane / 32;
+      const int c = (lane % 32) ^ (8 * (k >> 4));
+      off = (uint32_t)((int64_t)k * ld * 4 + c * 16);
+      ustep = (uint32_t)(2 * ld * 4);
+      kofs = 0;
+    }
+  }
+  __device__ uint32_t lds_of(int u) const {
+    return (uint32_t)((KMAJ ? 4 * u + wave : 4 * wave + u) * 1024);
+  }
+  // Loads of the k-step whose origin is `base` (`range` readable bytes) with
+  // `kv` valid reduction indices into the tile at `lds`.
+  __device__ void issue(const float* base, int64_t range, char* lds, int64_t kv) const {
+    const i32x4_t rs = make_rsrc(base, range);
+    const uint32_t l0 = lds_addr(lds);
+    uint32_t v = off;
+    if (KMAJ && kv < kF32BK && (int64_t)kofs >= kv) v = kOob;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      load16_to_lds(rs, v, __builtin_amdgcn_readfirstlane(l0 + lds_of(u)));
+      if (u + 1 < kPer) v = add_opaque(v, ustep);
+    }
+  }
+};
+
+template <bool KMAJ>
+struct F32Frag {
+  uint32_t base[2];  // per 32-row sub-tile t
+  __device__ void init(int row0, int lane) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = row0 + 32 * t + (lane & 31);
+      if (KMAJ) base[t] = (uint32_t)(r * 128 + ((4 * h) ^ ((r >> 1) & 7)) * 16);
+      else base[t] = (uint32_t)(16 * h * 512 + ((r >> 2) ^ (8 * h)) * 16 + (r & 3) * 4);
+    }
+  }
+  // K-major: floats for MFMAs 4q .. 4q+3 of sub-tile t.
+  __device__ f32x4_t read4(const char* lds, int t, int q) const {
+    // chunk (4h + q) ^ s == ((4h) ^ s) ^ q for q < 4 and s < 8
+    const uint32_t a = base[t] ^ (uint32_t)(q * 16);
+    return *reinterpret_cast<const f32x4_t*>(lds + a);
+  }
+  // MN-major: the float for MFMA j of sub-tile t (k-row 16h + j).
+  __device__ float read1(const char* lds, int t, int j) const {
+    return *reinterpret_cast<const float*>(lds + base[t] + j * 512);
+  }
+};
+
+template <int MODE, int EPI>
+__global__ void __launch_bounds__(kF32Waves * kWave, 2)
+gg_f32_mfma_kernel(GemmArgs g) {
+  constexpr bool kAK = MODE != kDw;   // A operand K-major?
+  constexpr bool kBKm = MODE == kDx;  // B operand K-major?
+  typedef F32Tile<kAK> TA;
+  typedef F32Tile<kBKm> TB;
+  constexpr int kStage = TA::kBytes + TB::kBytes;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+  __shared__ int32_t s_pref[2 * (NT_MAX_EXPERTS + 1)];
+
+  int64_t mtiles;
+  if (MODE != kDw) {
+    build_m_prefix(g.offsets, g.E, g.A, kF32BM, s_pref);
+    mtiles = s_pref[g.E];
+  } else {
+    build_chunk_prefix(g.offsets, g.E, g.A, 0, 0, 0, s_pref, s_pref + (NT_MAX_EXPERTS + 1));
+    mtiles = (int64_t)s_pref[g.E] * g.ntm;
+  }
+  const int64_t logical = blockIdx.x;
+  if (logical >= mtiles * g.ntn) return;
+  TileJobT<float> job;
+  setup_job<MODE, kF32BM, kF32BN, EPI, float>(g, s_pref, mtiles, logical, job);
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = wave / 2, wn = wave % 2;
+  TA ta;
+  TB tb;
+  ta.init(job.lda, wave, lane);
+  tb.init(job.ldb, wave, lane);
+  F32Frag<kAK> fa;
+  F32Frag<kBKm> fb;
+  fa.init(wm * 64, lane);
+  fb.init(wn * 64, lane);
+  const int64_t rv = job.rows_valid < kF32BM ? job.rows_valid : kF32BM;
+  const int64_t cv = job.cols_valid < kF32BN ? job.cols_valid : kF32BN;
+
+  // Stage kt. A two-part dX reduction takes nk1 = ceil(kred1 / BK) k-steps
+  // of (pa, pb), then those of (pa2, pb2): each part starts a k-step.
+  const int64_t nk1 = EPI == kEpiDualK ? ceil_div(job.kred1, kF32BK) : 0;
+  auto issue = [&](int64_t kt, char* lds) {
+    const float* a = job.pa;
+    const float* b = job.pb;
+    int64_t kl = kt * kF32BK, klen = job.kred;
+    if (EPI == kEpiDualK) {
+      klen = job.kred1;
+      if (kt >= nk1) {
+        a = job.pa2;
+        b = job.pb2;
+        kl = (kt - nk1) * kF32BK;
+        klen = job.kred - job.kred1;
+      }
+    }
+    const int64_t kleft = klen - kl;
+    const int64_t kv = kleft < kF32BK ? kleft : kF32BK;
+    const int64_t ra = kAK ? ((rv - 1) * job.lda + kv) * 4 : ((kv - 1) * job.lda + rv) * 4;
+    const int64_t rb = kBKm ? ((cv - 1) * job.ldb + kv) * 4 : ((kv - 1) * job.ldb + cv) * 4;
+    ta.issue(a + (kAK ? kl : kl * job.lda), ra, lds, kv);
+    tb.issue(b + (kBKm ? kl : kl * job.ldb), rb, lds + TA::kBytes, kv);
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk =
+      EPI == kEpiDualK ? nk1 + ceil_div(job.kred - job.kred1, kF32BK) : ceil_div(job.kred, kF32BK);
+  if (nk > 0) issue(0, smem);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    wait_vmcnt<0>();
+    __syncthreads();
+    const char* st = smem + (kt & 1) * kStage;
+    if (kt + 1 < nk) issue(kt + 1, smem + ((kt + 1) & 1) * kStage);
+    const char* sa = st;
+    const char* sb = st + TA::kBytes;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float av[2][4], bv[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (kAK) {
+          const f32x4_t x = fa.read4(sa, t, q);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) av[t][jj] = x[jj];
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) av[t][jj] = fa.read1(sa, t, 4 * q + jj);
+        }
+        if (kBKm) {
+          const f32x4_t x = fb.read4(sb, t, q);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) bv[t][jj] = x[jj];
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) bv[t][jj] = fb.read1(sb, t, 4 * q + jj);
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][jj], av[i][jj], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // acc[i][j][v] = C[m][n], m = 64 wm + 32 i + lane % 32, n = 64 wn + 32 j +
+  // 8 (v / 4) + 4 (lane / 32) + v % 4: four consecutive columns per group.
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = wm * 64 + i * 32 + (lane & 31);
+    if (m >= job.rows_valid) continue;
+    float* prow = job.po + (int64_t)m * job.ldo;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int n = wn * 64 + j * 32 + 8 * gq + 4 * (lane >> 5);
+        if (n >= job.cols_valid) continue;
+        const f32x4_t v = {acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                           acc[i][j][4 * gq + 3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(prow + n));
+      }
+  }
+}
+
 constexpr int kGT = 64;  // generic tile
 constexpr int kGK = 16;
 
@@ -1531,7 +1759,6 @@ bool mfma_ok(int dtype, int64_t K, int64_t N, const void* p0, const void* p1, co
   return al % 16 == 0;
 }
 
-// Compute units of the current device (cached per device id).
 // CUs of the device that `s` launches on (the null stream: the current
 // device). Concurrent first calls may both query; they store the same value.
 int device_cus(hipStream_t s) {
@@ -1841,6 +2068,30 @@ size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
   return (size_t)dw_slabs(A, dw_split(A, K, N, E)) * (size_t)(K * N * 4);
 }
 
+// fp32 MFMA kernel: 16-byte aligned operands and outputs, K and N multiples
+// of 4 (whole 16-byte chunks along every row).
+bool f32_mfma_ok(const GemmArgs& g, bool dual) {
+  if (g.K % 4 != 0 || g.N % 4 != 0) return false;
+  uintptr_t al = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b) |
+                 reinterpret_cast<uintptr_t>(g.out);
+  if (dual) al |= reinterpret_cast<uintptr_t>(g.a2) | reinterpret_cast<uintptr_t>(g.b2);
+  return al % 16 == 0;
+}
+
+template <int MODE, int EPI>
+int launch_f32_mfma(GemmArgs g, int64_t out_cols, hipStream_t s) {
+  g.chunk = 0;
+  const int64_t tiles = plan_tiles<MODE>(g, out_cols, kF32BM, kF32BN);
+  if (tiles == 0) return NT_OK;
+  if (tiles > INT32_MAX) return NT_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((gg_f32_mfma_kernel<MODE, EPI>), dim3((unsigned)tiles),
+                     dim3(kF32Waves * kWave), 0, s, g);
+  return launch_status();
+}
+
+template <int MODE>
+int launch_generic(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s);
+
 template <int MODE, int EPI>
 int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t s) {
   if (mfma) return launch_mfma_auto<MODE, EPI>(dtype, g, out_cols, s);
@@ -1869,6 +2120,23 @@ int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t 
     return launch_swiglu_elementwise<true>(dtype, g.out2, g.out, g.aux, g.aux2, g.A * out_cols,
                                            s);
   }
+  int st;
+  if (dtype == NT_F32 && f32_mfma_ok(g, EPI == kEpiDualK)) {
+    st = launch_f32_mfma<MODE, EPI == kEpiDualK ? kEpiDualK : kEpiPlain>(g, out_cols, s);
+  } else {
+    st = launch_generic<MODE>(dtype, g, out_cols, s);
+  }
+  if (st != NT_OK || (EPI != kEpiGelu && EPI != kEpiGeluGrad)) return st;
+  // Generic path: the GELU epilogue as a second, elementwise pass over the
+  // output rows (rows past offsets[E] hold unspecified values either way).
+  const int64_t n = g.A * out_cols;
+  if (EPI == kEpiGelu) return launch_gelu_elementwise<false>(dtype, g.out, g.out2, n, s);
+  return launch_gelu_elementwise<true>(dtype, g.out, const_cast<void*>(g.aux), n, s);
+}
+
+// The VALU kernel (any dtype, any shape; two-part dX when g.a2 is set).
+template <int MODE>
+int launch_generic(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   g.ntn = (int32_t)ceil_div(out_cols, kGT);
   int64_t nblocks;
   if (MODE == kDw) {
@@ -1888,13 +2156,7 @@ int launch_mode(int dtype, GemmArgs g, int64_t out_cols, bool mfma, hipStream_t 
     case NT_BF16: hipLaunchKernelGGL((gg_generic_kernel<bf16, MODE>), grid, dim3(256), 0, s, g); break;
     default: return NT_ERR_DTYPE;
   }
-  int st = launch_status();
-  if (st != NT_OK || (EPI != kEpiGelu && EPI != kEpiGeluGrad)) return st;
-  // Generic path: the GELU epilogue as a second, elementwise pass over the
-  // output rows (rows past offsets[E] hold unspecified values either way).
-  const int64_t n = g.A * out_cols;
-  if (EPI == kEpiGelu) return launch_gelu_elementwise<false>(dtype, g.out, g.out2, n, s);
-  return launch_gelu_elementwise<true>(dtype, g.out, const_cast<void*>(g.aux), n, s);
+  return launch_status();
 }
 
 // Argument check of one grouped GEMM of `mode`: fwd out[A,N] = a[A,K] b[E,K,N];

@@ -386,3 +386,32 @@ def test_dw_non_monotone_offsets_stay_in_the_workspace(ext, dtype):
         else:
             assert not dW[e].cpu().any(), e
     assert torch.equal(dW.cpu().view(torch.int16), dW2.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("K,N", [(4, 4), (36, 20), (100, 132), (260, 4), (512, 2048)])
+@pytest.mark.parametrize("counts", [[0, 5, 0, 130, 1, 0], [257, 0, 300], [1, 1, 1, 1]])
+def test_f32_mfma_tails_and_empty_experts(ext, K, N, counts):
+    """fp32 on the MFMA kernel (K, N multiples of 4): reduction tails of 4,
+    ragged column tiles, empty experts (dW exactly zero), M_e = 1, and the
+    two-part dX of the SwiGLU backward against the sum of two oracle dX."""
+    dtype = torch.float32
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    A = int(offsets[-1]) + 3
+    g = torch.Generator().manual_seed(K * 7 + N + len(counts))
+    X = torch.randn(A, K, generator=g)
+    W = torch.randn(len(counts), K, N, generator=g) / K ** 0.5
+    W2 = torch.randn(len(counts), K, N, generator=g) / K ** 0.5
+    G = torch.randn(A, N, generator=g)
+    G2 = torch.randn(A, N, generator=g)
+    out, dX, dW = run_all(ext, X, W, offsets, G)
+    dX2 = ext.bwd_grouped_gemm_dX2(W.cuda(), W2.cuda(), offsets.cuda(), G.cuda(), G2.cuda())
+    torch.cuda.synchronize()
+    used = int(offsets[-1])
+    check(out[:used], O.grouped_gemm(X, offsets, W)[:used], dtype, scale=max(1, K) ** 0.5)
+    check(dX[:used], O.grouped_gemm_dx(W, offsets, G)[:used], dtype, scale=max(1, N) ** 0.5)
+    want2 = O.grouped_gemm_dx(W, offsets, G) + O.grouped_gemm_dx(W2, offsets, G2)
+    check(dX2[:used], want2[:used], dtype, scale=(2 * max(1, N)) ** 0.5)
+    check(dW, O.grouped_gemm_dw(X, offsets, G), dtype, scale=max(counts + [1]) ** 0.5)
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert not dW[e].any()
