@@ -115,14 +115,18 @@ constexpr int kRowBatch = 16;  // rows in flight per wave in the short-row copy
 
 // Rank, place and copy. base_mode 0: base[e] comes from `base` (cursor copy);
 // base_mode 1: base[e] = exclusive scan of counts (offsets), written to
-// `offsets` by workgroup 0.
+// `offsets` by workgroup 0; `hist` holds the per-expert exclusive scans over
+// blocks (scan_kernel). base_mode 2 (no scan launch): `hist` holds the raw
+// per-block counts; every workgroup sums expert e's row of it (wave e mod 4)
+// into its total and the part before this block, and workgroup 0 writes
+// counts and offsets.
 template <typename V>
 __global__ void __launch_bounds__(kDispatchThreads)
 pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
                  const int32_t* __restrict__ topk, int64_t T, int32_t k, int32_t E,
                  int32_t nbits, int32_t TB, int32_t nb, int64_t nv, int64_t A_cap,
                  const int32_t* __restrict__ hist, int base_mode,
-                 const int32_t* __restrict__ base, const int32_t* __restrict__ counts,
+                 const int32_t* __restrict__ base, int32_t* __restrict__ counts,
                  int32_t* __restrict__ offsets, V* __restrict__ packed_X,
                  int32_t* __restrict__ token_id, int32_t* __restrict__ expert,
                  float* __restrict__ packed_w, int32_t* __restrict__ inv) {
@@ -137,9 +141,76 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
   const int lane = lane_id();
   const int wave = tid / kWave;
 
+  const int64_t tok0 = (int64_t)b * TB;
+  const int ntok = (int)min((int64_t)TB, T - tok0);
+  const int na = ntok * k;
+  const int64_t f0 = tok0 * k;
+
+  // Short rows (one 16-byte vector per lane): the wave's first kRowBatch
+  // token rows are loaded before the bases and the ranking, so their latency
+  // hides behind them; only the store addresses depend on the ranks.
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr bool kVec16 = sizeof(V) == 16;
+  const bool short_rows = kVec16 && nv > 0 && nv <= kWave;
+  const bool on = lane < nv;
+  u32x4 pre[kRowBatch];
+  if (short_rows) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(X);
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      const int tt = wave + u * kDispatchWaves;
+      if (on && tt < ntok) pre[u] = load_nt(src + (tok0 + tt) * nv + lane);
+    }
+  }
+
   // Per-expert base of this block.
   if (base_mode == 0) {
     for (int e = tid; e < E; e += kDispatchThreads) s_base[e] = base[e];
+  } else if (base_mode == 2) {
+    for (int e = wave; e < E; e += kDispatchWaves) {
+      const int32_t* h = hist + (int64_t)e * nb;
+      int tot = 0, before = 0;
+      // Eight loads in flight per lane (the entries are L2-resident).
+      for (int i0 = 0; i0 < nb; i0 += 8 * kWave) {
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * kWave + lane;
+          v[u] = i < nb ? h[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int i = i0 + u * kWave + lane;
+          tot += v[u];
+          before += i < b ? v[u] : 0;
+        }
+      }
+      tot = wave_sum_int(tot);
+      before = wave_sum_int(before);
+      if (lane == 0) {
+        s_run[e] = tot;
+        s_base[e] = before;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      int carry = 0;
+      for (int s0 = 0; s0 < E; s0 += kWave) {
+        const int e = s0 + lane;
+        const int v = e < E ? s_run[e] : 0;
+        const int incl = wave_incl_scan(v);
+        if (e < E) {
+          s_base[e] += carry + incl - v;
+          if (b == 0) {
+            counts[e] = v;
+            offsets[e] = carry + incl - v;
+          }
+        }
+        carry += __shfl(incl, kWave - 1, kWave);
+      }
+      if (b == 0 && lane == 0) offsets[E] = carry;
+    }
+    __syncthreads();
   } else {
     // Exclusive scan of counts over experts (E <= NT_MAX_EXPERTS) in s_base.
     for (int e = tid; e < E; e += kDispatchThreads) s_base[e] = counts[e];
@@ -161,33 +232,12 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
     __syncthreads();
   }
   for (int e = tid; e < E; e += kDispatchThreads) {
-    s_base[e] += hist[(int64_t)e * nb + b];
+    if (base_mode != 2) s_base[e] += hist[(int64_t)e * nb + b];
     s_run[e] = 0;
   }
   for (int i = tid; i < kDispatchWaves * E; i += kDispatchThreads) s_wc[i] = 0;
   __syncthreads();
 
-  const int64_t tok0 = (int64_t)b * TB;
-  const int ntok = (int)min((int64_t)TB, T - tok0);
-  const int na = ntok * k;
-  const int64_t f0 = tok0 * k;
-
-  // Short rows (one 16-byte vector per lane): the wave's first kRowBatch
-  // token rows are loaded before the ranking, so their latency hides behind
-  // it; only the store addresses depend on the ranks.
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr bool kVec16 = sizeof(V) == 16;
-  const bool short_rows = kVec16 && nv > 0 && nv <= kWave;
-  const bool on = lane < nv;
-  u32x4 pre[kRowBatch];
-  if (short_rows) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(X);
-#pragma unroll
-    for (int u = 0; u < kRowBatch; ++u) {
-      const int tt = wave + u * kDispatchWaves;
-      if (on && tt < ntok) pre[u] = load_nt(src + (tok0 + tt) * nv + lane);
-    }
-  }
 
   // Stable rank of each assignment among same-expert assignments of the block.
   for (int r = 0; r < na; r += kDispatchThreads) {
@@ -301,7 +351,7 @@ size_t pack_lds_bytes(const PackPlan& p, int32_t E, int32_t k) {
 template <typename V>
 int launch_pack_rows(const PackPlan& plan, const void* X, const float* w, const int32_t* topk,
                      int64_t T, int32_t k, int32_t E, const int32_t* hist, int base_mode,
-                     const int32_t* base, const int32_t* counts, int32_t* offsets,
+                     const int32_t* base, int32_t* counts, int32_t* offsets,
                      void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
                      int32_t* inv, hipStream_t stream) {
   const int64_t nv = plan.row_bytes / (int64_t)sizeof(V);
@@ -315,7 +365,7 @@ int launch_pack_rows(const PackPlan& plan, const void* X, const float* w, const 
 
 int pack_rows_dispatch(const PackPlan& plan, const void* X, void* packed_X, const float* w,
                        const int32_t* topk, int64_t T, int32_t k, int32_t E, const int32_t* hist,
-                       int base_mode, const int32_t* base, const int32_t* counts,
+                       int base_mode, const int32_t* base, int32_t* counts,
                        int32_t* offsets, int32_t* token_id, int32_t* expert, float* packed_w,
                        int32_t* inv, hipStream_t stream) {
   const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(packed_X) |
@@ -409,7 +459,10 @@ namespace {
 
 // nt_dispatch / nt_dispatch_counted: counted = the per-block histogram is
 // already in ws (written by nt_route_topk_count); otherwise hist_kernel
-// builds it.
+// builds it. Up to kFoldMaxEntries histogram entries (E * blocks: C1, C2 and
+// C4 of the configs) the pack workgroups sum it themselves, each reading it
+// whole from L2, instead of a scan launch.
+constexpr int64_t kFoldMaxEntries = 8192;
 int dispatch_impl(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
                   int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
                   void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
@@ -425,7 +478,16 @@ int dispatch_impl(int dtype, const void* X, const float* w, const int32_t* topk,
   const PackPlan plan = plan_pack(T, k, d * eb);
   if (ws == nullptr || ws_bytes < dispatch_ws_bytes(plan, E)) return NT_ERR_WORKSPACE;
   int32_t* hist = static_cast<int32_t*>(ws);
-  if (counted) {
+  // Small histograms are summed inside the pack (base_mode 2): no scan launch.
+  const bool fold = plan.nb > 0 && (int64_t)E * plan.nb <= kFoldMaxEntries;
+  if (fold) {
+    st = NT_OK;
+    if (!counted) {
+      hipLaunchKernelGGL(hist_kernel, dim3(plan.nb), dim3(kDispatchThreads), (size_t)E * 4,
+                         stream, topk, nullptr, T, k, E, plan.TB, plan.nb, hist);
+      st = launch_status();
+    }
+  } else if (counted) {
     hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, plan.nb,
                        counts, nullptr, nullptr);
     st = launch_status();
@@ -439,8 +501,8 @@ int dispatch_impl(int dtype, const void* X, const float* w, const int32_t* topk,
                        (int64_t)E + 1, 0);
     return launch_status();
   }
-  return pack_rows_dispatch(plan, X, packed_X, w, topk, T, k, E, hist, 1, nullptr, counts,
-                            offsets, token_id, expert, packed_w, inv, stream);
+  return pack_rows_dispatch(plan, X, packed_X, w, topk, T, k, E, hist, fold ? 2 : 1, nullptr,
+                            counts, offsets, token_id, expert, packed_w, inv, stream);
 }
 
 }  // namespace
