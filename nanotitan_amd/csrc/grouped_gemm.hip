@@ -1091,6 +1091,9 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   constexpr int TM = WM / 32, TN = WN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
   static_assert(NS >= 2, "at least two LDS stages");
+  // Only the 64-deep k-step is built and tested: a 32-deep variant (measured
+  // at C3 and C4, slower) gave results that differ from it.
+  static_assert(BK == 64, "k-step depth 64");
   constexpr bool kAK = MODE != kDw;   // A operand K-major?
   constexpr bool kBKm = MODE == kDx;  // B operand K-major?
   constexpr int kDual = EPI == kEpiSwiGLU ? 1 : (EPI == kEpiDualK ? 2 : 0);
