@@ -59,6 +59,8 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+from bench_profiles import kernel_source_hash  # noqa: E402
+
 METRIC = "MoE layer fwd+bwd tokens/sec (1×MI355X); pack/combine HBM GB/s; GEMM MFMA %"
 PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {torch.bfloat16: 2500.0, torch.float16: 2500.0, torch.float32: 157.3}
@@ -483,8 +485,9 @@ def cpu_baseline(wl_cpu, budget_s: float = 20.0):
 
 def profile_fields(wl, ffn_kind):
     """HBM traffic and MFMA busy fraction of the GEMMs from the committed
-    rocprofv3 counter summaries (profiles/*.json), tagged with the commit whose
-    kernels they were measured on."""
+    rocprofv3 counter summaries (profiles/*.json, written by bench_profiles.py),
+    tagged with the commit whose kernels they were measured on and marked
+    stale when the kernel sources have changed since."""
     out = {}
     if ffn_kind != "gelu":
         return out
@@ -506,21 +509,27 @@ def profile_fields(wl, ffn_kind):
             out["traffic"] = round(sum(fams_t[f]["bytes"] * c for f, c in per_step.items()) / n)
             out["traffic_algorithmic"] = round(
                 sum(fams_t[f]["algorithmic_bytes"] * c for f, c in per_step.items()) / n)
-            out["traffic_source"] = f"profiles/{prof.name} (kernels of commit " \
-                                    f"{js.get('commit', 'unrecorded')})"
+            out["traffic_source"] = source_note(prof, js)
     mf = ROOT / "profiles" / f"mfma_{wl['name'].lower()}.json"
     if mf.exists():
         js = json.loads(mf.read_text())
-        fam_m = {k: v for k, v in js.items() if isinstance(v, dict)}
+        fam_m = js.get("families", {})
         t_all = sum(v["launches"] * v["avg_us"] for v in fam_m.values())
         if t_all > 0:
             def tw(key):
                 return sum(v[key] * v["launches"] * v["avg_us"] for v in fam_m.values()) / t_all
             out["mfma_busy_frac"] = round(tw("mfma_busy_frac"), 4)
             out["clock_ghz"] = round(tw("clock_ghz"), 3)
-            out["mfma_source"] = f"profiles/{mf.name} (kernels of commit " \
-                                 f"{js.get('commit', 'unrecorded')})"
+            out["mfma_source"] = source_note(mf, js)
     return out
+
+
+def source_note(path, js):
+    """Where a profile figure comes from, and whether the kernel sources it
+    was measured on are the ones this run executes."""
+    same = js.get("source_hash") == kernel_source_hash(ROOT)
+    return (f"profiles/{path.name}, kernels of commit {js.get('commit', 'unrecorded')}"
+            f"{'' if same else ' (kernel sources changed since: stale)'}")
 
 
 def main():
