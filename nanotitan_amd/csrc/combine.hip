@@ -28,6 +28,10 @@ constexpr int kMaxSorted = 256;
 // k <= 8).
 constexpr int kCombineU = 1;
 constexpr int kPackBwdU = 2;
+// Rows beyond one 16-byte vector per lane: one token per wave (measured
+// cold, C4 8 KiB rows: 80 -> 75 us against two).
+constexpr int kPackBwdULong = 1;
+constexpr int64_t kLongRowBytes = 1024;
 constexpr int fan_u(int kmax, int u) { return kmax <= 2 ? u : 1; }
 
 template <typename S, int N>
@@ -773,8 +777,14 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   const S* ip = static_cast<const S*>(dpX);
   S* op = static_cast<S*>(dX);
   if (src.start == nullptr && expert == nullptr && k <= 8) {
-#define NT_PBI(VE, KM) \
-  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, kPackBwdU)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kPackBwdU))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
+    const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
+#define NT_PBI_U(VE, KM, U) \
+  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
+#define NT_PBI(VE, KM)                           \
+  do {                                           \
+    if (long_rows) NT_PBI_U(VE, KM, kPackBwdULong); \
+    else NT_PBI_U(VE, KM, kPackBwdU);            \
+  } while (0)
 #define NT_PBI_VE(KM)            \
   switch (ve) {                  \
     case 8: NT_PBI(8, KM); break; \
@@ -789,6 +799,7 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
     }
 #undef NT_PBI_VE
 #undef NT_PBI
+#undef NT_PBI_U
     return launch_status();
   }
   switch (ve) {

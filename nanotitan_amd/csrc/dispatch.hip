@@ -100,7 +100,9 @@ scan_kernel(int32_t* __restrict__ hist, int32_t nb, int32_t* __restrict__ counts
 
 // Long rows: each lane loads up to kLongRowBatch 16-byte vectors of a row
 // before it stores any (measured cold: C4 8 KiB rows 89 -> 78 us, C5 4 KiB
-// rows 555 -> 497 us against one vector at a time).
+// rows 555 -> 497 us against one vector at a time; with the long-row
+// instantiation at 8 waves per SIMD, C4 78 -> 76 us, and 4 or 16 vectors
+// the same).
 constexpr int kLongRowBatch = 8;
 
 template <typename V>
@@ -135,7 +137,10 @@ constexpr int kRowBatch = 16;  // rows in flight per wave in the short-row copy
 // per-block counts; every workgroup sums expert e's row of it (wave e mod 4)
 // into its total and the part before this block, and workgroup 0 writes
 // counts and offsets.
-template <typename V>
+// SHORT: the instantiation for rows of one 16-byte vector per lane or less
+// (its 16-row batches hold 128 registers, which would cap the long-row copy
+// at two waves per SIMD).
+template <typename V, bool SHORT>
 __global__ void __launch_bounds__(kDispatchThreads)
 pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
                  const int32_t* __restrict__ topk, int64_t T, int32_t k, int32_t E,
@@ -165,7 +170,7 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
   // token rows are loaded before the bases and the ranking, so their latency
   // hides behind them; only the store addresses depend on the ranks.
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr bool kVec16 = sizeof(V) == 16;
+  constexpr bool kVec16 = sizeof(V) == 16 && SHORT;
   const bool short_rows = kVec16 && nv > 0 && nv <= kWave;
   const bool on = lane < nv;
   u32x4 pre[kRowBatch];
@@ -379,7 +384,9 @@ int launch_pack_rows(const PackPlan& plan, const void* X, const float* w, const 
                      int32_t* inv, hipStream_t stream) {
   const int64_t nv = plan.row_bytes / (int64_t)sizeof(V);
   const size_t lds = pack_lds_bytes(plan, E, k);
-  hipLaunchKernelGGL(pack_rows_kernel<V>, dim3(plan.nb), dim3(kDispatchThreads), lds, stream,
+  auto kern = sizeof(V) == 16 && nv > 0 && nv <= kWave ? pack_rows_kernel<V, true>
+                                                      : pack_rows_kernel<V, false>;
+  hipLaunchKernelGGL(kern, dim3(plan.nb), dim3(kDispatchThreads), lds, stream,
                      static_cast<const V*>(X), w, topk, T, k, E, nbits_for(E), plan.TB, plan.nb,
                      nv, T * k, hist, base_mode, base, counts, offsets, static_cast<V*>(packed_X),
                      token_id, expert, packed_w, inv);
