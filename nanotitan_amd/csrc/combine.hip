@@ -52,6 +52,45 @@ __device__ __forceinline__ void load_vec(const typename elem<T>::storage* p, flo
   for (int i = 0; i < VE; ++i) out[i] = elem<T>::load(v.v[i]);
 }
 
+// The same load kept as the raw word (VE 16-bit elements take half the
+// registers of VE floats), converted by unpack_vec where it is summed: the
+// gathers that hold k rows in flight then keep their occupancy.
+template <typename T, int VE>
+using raw_vec = typename nt_word<sizeof(typename elem<T>::storage) * VE>::type;
+template <typename T, int VE>
+__device__ __forceinline__ raw_vec<T, VE> load_raw(const typename elem<T>::storage* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const raw_vec<T, VE>*>(p));
+}
+template <typename T, int VE>
+__device__ __forceinline__ void unpack_vec(raw_vec<T, VE> w, float (&out)[VE]) {
+  using S = typename elem<T>::storage;
+  const vpack<S, VE> v = __builtin_bit_cast(vpack<S, VE>, w);
+#pragma unroll
+  for (int i = 0; i < VE; ++i) out[i] = elem<T>::load(v.v[i]);
+}
+
+// One gathered row chunk of a wave's k rows: the raw word (RAW) or floats.
+// Raw words halve the registers of 16-bit rows, which keeps the k = 8
+// gathers and the short rows at full occupancy; with k <= 2 and long rows
+// the float form was faster (measured cold at C4: combine 75 vs 78 us).
+template <typename T, int VE, bool RAW>
+struct RowBuf;
+template <typename T, int VE>
+struct RowBuf<T, VE, true> {
+  raw_vec<T, VE> w;
+  __device__ void load(const typename elem<T>::storage* p) { w = load_raw<T, VE>(p); }
+  __device__ void get(float (&out)[VE]) const { unpack_vec<T, VE>(w, out); }
+};
+template <typename T, int VE>
+struct RowBuf<T, VE, false> {
+  float f[VE];
+  __device__ void load(const typename elem<T>::storage* p) { load_vec<T, VE>(p, f); }
+  __device__ void get(float (&out)[VE]) const {
+#pragma unroll
+    for (int v = 0; v < VE; ++v) out[v] = f[v];
+  }
+};
+
 template <typename T, int VE>
 __device__ __forceinline__ void store_vec(typename elem<T>::storage* p, const float (&in)[VE]) {
   using S = typename elem<T>::storage;
@@ -402,7 +441,7 @@ __device__ __forceinline__ void sorted_slots(const int32_t* __restrict__ inv, in
   }
 }
 
-template <typename T, typename TO, int VE, int KMAX, int U>
+template <typename T, typename TO, int VE, int KMAX, int U, bool RAW>
 __global__ void __launch_bounds__(kThreads)
 combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
                    const int32_t* __restrict__ inv, int32_t k, const float* __restrict__ w,
@@ -420,12 +459,12 @@ combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) wp[u][j] = j < n[u] ? w[p[u][j]] : 0.f;
   for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
-    float x[U][KMAX][VE];
+    RowBuf<T, VE, RAW> x[U][KMAX];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < KMAX; ++j)
-        if (j < n[u]) load_vec<T, VE>(y + (int64_t)p[u][j] * d + h, x[u][j]);
+        if (j < n[u]) x[u][j].load(y + (int64_t)p[u][j] * d + h);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (t0 + u >= T_) break;
@@ -436,9 +475,12 @@ combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
 #pragma clang fp contract(off)
 #pragma unroll
         for (int j = 0; j < KMAX; ++j)
-          if (j < n[u])
+          if (j < n[u]) {
+            float xf[VE];
+            x[u][j].get(xf);
 #pragma unroll
-            for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp[u][j] * x[u][j][v];
+            for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp[u][j] * xf[v];
+          }
       }
       store_vec<TO, VE>(out + (t0 + u) * d + h, acc);
     }
@@ -596,7 +638,7 @@ pack_bwd_kernel(const typename elem<T>::storage* __restrict__ dpX, const float* 
 // Inverse-map pack backward for small fan-in: same sums as pack_bwd_kernel
 // (ascending packed order, fp32), U tokens per wave with every row load
 // issued up front.
-template <typename T, int VE, int KMAX, int U>
+template <typename T, int VE, int KMAX, int U, bool RAW>
 __global__ void __launch_bounds__(kThreads)
 pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
                     const float* __restrict__ dpw, const int32_t* __restrict__ inv,
@@ -617,12 +659,12 @@ pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
     if (jl < k && tl < T_) dw[tl * k + jl] = (mine >= 0 && mine < rows) ? dpw[mine] : 0.f;
   }
   for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
-    float x[U][KMAX][VE];
+    RowBuf<T, VE, RAW> x[U][KMAX];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < KMAX; ++j)
-        if (j < n[u]) load_vec<T, VE>(dpX + (int64_t)p[u][j] * d + h, x[u][j]);
+        if (j < n[u]) x[u][j].load(dpX + (int64_t)p[u][j] * d + h);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (t0 + u >= T_) break;
@@ -631,9 +673,12 @@ pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
       for (int v = 0; v < VE; ++v) acc[v] = 0.f;
 #pragma unroll
       for (int j = 0; j < KMAX; ++j)
-        if (j < n[u])
+        if (j < n[u]) {
+          float xf[VE];
+          x[u][j].get(xf);
 #pragma unroll
-          for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], x[u][j][v]);
+          for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], xf[v]);
+        }
       store_vec<T, VE>(dX + (t0 + u) * d + h, acc);
     }
   }
@@ -664,8 +709,14 @@ int run_combine(const void* y, ListSrc src, const float* w, int64_t T_, int64_t 
   const S* yp = static_cast<const S*>(y);
   SO* op = static_cast<SO*>(out);
   if (src.start == nullptr && src.k <= 8) {
+    const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
 #define NT_CI(VE, KM) \
-  hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op)
+  do {                                                                                   \
+    if (KM <= 2 && long_rows)                                                            \
+      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), false>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
+    else                                                                                 \
+      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), true>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
+  } while (0)
 #define NT_CI_VE(KM)            \
   switch (ve) {                 \
     case 8: NT_CI(8, KM); break; \
@@ -778,12 +829,13 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   S* op = static_cast<S*>(dX);
   if (src.start == nullptr && expert == nullptr && k <= 8) {
     const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
-#define NT_PBI_U(VE, KM, U) \
-  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U)>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
-#define NT_PBI(VE, KM)                           \
-  do {                                           \
-    if (long_rows) NT_PBI_U(VE, KM, kPackBwdULong); \
-    else NT_PBI_U(VE, KM, kPackBwdU);            \
+#define NT_PBI_U(VE, KM, U, RAW) \
+  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U), RAW>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
+#define NT_PBI(VE, KM)                                                    \
+  do {                                                                    \
+    if (long_rows && KM <= 2) NT_PBI_U(VE, KM, kPackBwdULong, false);     \
+    else if (long_rows) NT_PBI_U(VE, KM, kPackBwdULong, true);            \
+    else NT_PBI_U(VE, KM, kPackBwdU, true);                               \
   } while (0)
 #define NT_PBI_VE(KM)            \
   switch (ve) {                  \
