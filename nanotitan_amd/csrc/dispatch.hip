@@ -333,10 +333,9 @@ struct PackPlan {
 constexpr int64_t kMinLongRowBlocks = 512;
 
 PackPlan plan_pack(int64_t T, int32_t k, int64_t row_bytes) {
-  int32_t tb = 64;
-  if (row_bytes >= 8192) tb = 16;
-  else if (row_bytes >= 4096) tb = 16;
-  else if (row_bytes >= 2048) tb = 32;
+  // Rows of 2 KiB and more: 32 tokens per block (measured cold against 16
+  // and 8: C4 75.6 -> 74.5 us, C5 499 -> 493 us; 64 the same as 32).
+  int32_t tb = row_bytes >= 2048 ? 32 : 64;
   while (tb > 1 && (int64_t)tb * k > 2048) tb >>= 1;
   // Long rows (beyond one 16-byte vector per lane) with few tokens: at least
   // two blocks per CU (measured cold, C1 at 2 KiB rows: 22.6 -> 17.2 us).

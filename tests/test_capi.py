@@ -42,12 +42,14 @@ def test_strerror_and_version():
 
 
 def test_dispatch_block_tokens():
-    """The router's count blocks follow the pack's: fewer tokens per block for wider rows."""
+    """The router's count blocks follow the pack's: 64 tokens per block for rows up to
+    1 KiB, 32 for wider rows, fewer when that leaves under 512 blocks of long rows."""
     lib = capi.load()
     bt = lib.nt_dispatch_block_tokens
-    assert bt(30720, 2, 4096, capi.NT_BF16) == 16
+    assert bt(30720, 2, 4096, capi.NT_BF16) == 32
     assert bt(30720, 2, 512, capi.NT_BF16) == 64
-    assert bt(30720, 2, 1024, capi.NT_F32) < bt(30720, 2, 1024, capi.NT_BF16)
+    assert bt(30720, 2, 1024, capi.NT_F32) < bt(30720, 2, 256, capi.NT_BF16)
+    assert bt(4096, 2, 512, capi.NT_F32) == 8  # C1: 512 blocks of 2 KiB rows
     assert bt(100, 32, 8, capi.NT_F32) * 32 <= 2048
     assert bt(100, 0, 8, capi.NT_F32) == 0
     assert bt(100, 2, 8, 99) == 0
