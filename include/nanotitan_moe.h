@@ -237,7 +237,10 @@ int nt_route_topk_backward(const float* gates, const int32_t* topk, const float*
  * bytes of tile counters (paired calls), then the fp32 partial sums of
  * experts whose reduction is split (skewed routing): at most 256 MiB plus
  * one K*N*4 slab; 256 bytes when no split can occur. A smaller or NULL
- * workspace is accepted: dW then runs unsplit (and unpaired). */
+ * workspace is accepted: dW then runs unsplit (and unpaired). Its contents
+ * need no initialisation: the counters carry a per-launch tag, and every
+ * slab a launch reads it has written. Calls that overlap in time must not
+ * share a workspace. */
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N);
 
 /* out[a,:] = X[a,:] @ W[e] for a in [offsets[e], offsets[e+1]), float32

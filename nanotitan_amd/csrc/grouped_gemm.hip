@@ -20,6 +20,7 @@
 // LDS-tiled FMA kernel with the same scheduler.
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1080,13 +1081,41 @@ struct GemmLds {
   static constexpr int kTabWords = kTab ? kGeluTabWords : 1;
 };
 
+// The next of `limit` items from a counter tagged with the launch's epoch:
+// high 40 bits the epoch, low 24 the number of claims so far. A claim is one
+// atomic add. An add that finds a word from before this launch (another
+// epoch: an earlier launch's count, or any other leftover data) installs
+// this launch's epoch with one claim taken, by compare-and-swap; if another
+// workgroup installed it first, the claim is counted again by an add. So the
+// counters need no clearing before a launch, and only the first claims of a
+// launch can take more than one atomic.
+constexpr int kClaimBits = 24;
+__device__ int64_t claim_tagged(unsigned long long* ctr, unsigned long long epoch,
+                                int64_t limit) {
+  constexpr unsigned long long kCount = (1ull << kClaimBits) - 1;
+  unsigned long long v = atomicAdd(ctr, 1ull);
+  while ((v >> kClaimBits) != epoch) {
+    const unsigned long long cur =
+        __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((cur >> kClaimBits) == epoch) {
+      v = atomicAdd(ctr, 1ull);
+    } else if (atomicCAS(ctr, cur, (epoch << kClaimBits) | 1ull) == cur) {
+      return limit > 0 ? 0 : -1;
+    }
+  }
+  const int64_t cnt = (int64_t)(v & kCount);
+  return cnt < limit ? cnt : -1;
+}
+
 // The tile loop of workgroup `wg` of `G` that share this GEMM (the kernel's
 // body; gg_pair_kernel runs two of them side by side).
 template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
           bool SPLIT, bool DYN = false>
 __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_t G, char* smem,
                                            int32_t* s_pref, uint32_t* s_gtab,
-                                           int32_t* dyn = nullptr, int64_t* s_next = nullptr) {
+                                           unsigned long long* dyn = nullptr,
+                                           int64_t* s_next = nullptr,
+                                           unsigned long long epoch = 0) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -1131,16 +1160,16 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   const int64_t t_end = total * (before + nbx) / G;
   int64_t logical = total * before / G + wg / kXcd;
   // Dynamic order (DYN): the tiles form kXcd contiguous parts;
-  // workgroup wg takes the next tile of its XCD's part from counter dyn[p]
-  // (zeroed before the launch), then those of the following parts. One
+  // workgroup wg takes the next tile of its XCD's part from the epoch-tagged
+  // counter dyn[p] (claim_tagged), then those of the following parts. One
   // thread claims, the LDS slot *s_next publishes it at a barrier.
   auto claim = [&]() -> int64_t {
     for (int i = 0; i < kXcd; ++i) {
       const int p = (xcd + i) % kXcd;
       const int64_t p0 = total * p / kXcd, p1 = total * (p + 1) / kXcd;
       if (p1 <= p0) continue;
-      const int64_t c = atomicAdd(dyn + p, 1);
-      if (c < p1 - p0) return p0 + c;
+      const int64_t c = claim_tagged(dyn + p, epoch, p1 - p0);
+      if (c >= 0) return p0 + c;
     }
     return -1;
   };
@@ -1387,10 +1416,12 @@ gg_mfma_kernel(GemmArgs g) {
 // keep the device busy while the dW's run, and any imbalance in the dW (a
 // skewed expert's chunks) is absorbed. Both on 256x256 tiles with 8 waves;
 // nw is a multiple of 8, so the dW part keeps the XCD mapping (workgroup b
-// runs on XCD b % 8). dyn: kXcd zeroed counters.
+// runs on XCD b % 8). dyn: kXcd claim counters (claim_tagged, with this
+// launch's epoch).
 template <typename T, int EPIX, bool SPLITX>
 __global__ void __launch_bounds__(8 * kWave)
-gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, int32_t* dyn) {
+gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, unsigned long long* dyn,
+               unsigned long long epoch) {
   typedef GemmLds<T, kDw, 256, 256, 2, 4, 64, 2, kEpiPlain, false> LW;
   typedef GemmLds<T, kDx, 256, 256, 2, 4, 64, 2, EPIX, SPLITX> LX;
   static_assert(!LX::kTab, "no GELU table in the pair kernel");
@@ -1404,11 +1435,7 @@ gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, int32_t* dyn) {
     __syncthreads();  // LDS is reused by the dX tiles below
   }
   gemm_tiles<T, kDx, 256, 256, 2, 4, 64, 2, EPIX, SPLITX, true>(gx, blockIdx.x, gridDim.x, smem,
-                                                              s_pref, s_gtab, dyn, &s_next);
-}
-
-__global__ void zero_i32_kernel(int32_t* p, int n) {
-  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+                                                              s_pref, s_gtab, dyn, &s_next, epoch);
 }
 
 // ------------------------------------------------------- generic FMA kernel
@@ -2290,6 +2317,23 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
 // order).
 constexpr int32_t kPairMaxExperts = 16;
 
+// Epochs of the paired launches' claim counters: 40 bits, a different
+// value per launch in this process, starting from a value drawn from the
+// clock and this library's load address (so leftover data from another
+// process is unlikely to carry it), never 0.
+unsigned long long next_claim_epoch() {
+  constexpr unsigned long long kMask = (1ull << (64 - kClaimBits)) - 1;
+  static std::atomic<unsigned long long> next{
+      (static_cast<unsigned long long>(
+           std::chrono::steady_clock::now().time_since_epoch().count()) *
+           0x9E3779B97F4A7C15ull ^
+       reinterpret_cast<uintptr_t>(&next)) &
+      kMask};
+  unsigned long long e = next.fetch_add(1, std::memory_order_relaxed) & kMask;
+  if (e == 0) e = next.fetch_add(1, std::memory_order_relaxed) & kMask;
+  return e;
+}
+
 template <int EPIX>
 int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOut, int32_t E,
                int64_t A, int64_t K, int64_t N, void* dW, void* ws, size_t ws_bytes,
@@ -2311,7 +2355,11 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   // layer step paired), while 128x128 tiles balance it.
   const bool pair = mfma_dw && dx_mfma && A > 0 && K > 0 && N > 0 && aligned &&
                     ws_bytes >= kCtrBytes && E <= kPairMaxExperts && dw_tiles * 2 < cus * 3 &&
-                    nw <= cus - cus / 4 && cus % 8 == 0;
+                    nw <= cus - cus / 4 && cus % 8 == 0 &&
+                    // claim counts stay below 2^kClaimBits: every tile once, plus
+                    // at most one failed claim per part per claim call
+                    ((ceil_div(A, 256) + E) * ceil_div(K, 256) + 64) * 9 <
+                        (int64_t{1} << kClaimBits);
   if (!pair) {
     const int st = dw_impl(dtype, X, offsets, dOut, E, A, K, N, dW, ws, ws_bytes, stream);
     if (st != NT_OK) return st;
@@ -2325,8 +2373,8 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
     gw.slab_cap = (int32_t)dw_slabs(A, sp);
     gw.partial = partial;
   }
-  int32_t* dyn = static_cast<int32_t*>(ws);
-  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(kWave), 0, stream, dyn, 8);
+  unsigned long long* dyn = static_cast<unsigned long long*>(ws);
+  const unsigned long long epoch = next_claim_epoch();
   plan_tiles<kDw>(gw, N, 256, 256);
   plan_tiles<kDx>(gx, K, 256, 256);
   // split duties for the dX as launch_mfma_auto would choose them
@@ -2338,16 +2386,16 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   if (dtype == NT_BF16) {
     if (splitx) {
       if constexpr (kPlain)
-        hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn);
+        hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn, epoch);
     } else {
-      hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn);
+      hipLaunchKernelGGL((gg_pair_kernel<bf16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn, epoch);
     }
   } else {
     if (splitx) {
       if constexpr (kPlain)
-        hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn);
+        hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, true>), grid, block, 0, stream, gw, gx, nw32, dyn, epoch);
     } else {
-      hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn);
+      hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn, epoch);
     }
   }
   int st = launch_status();
