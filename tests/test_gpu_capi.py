@@ -143,3 +143,41 @@ def test_capi_grouped_gemm_three_ops(lib, dtype):
                                O.grouped_gemm_dw(X, offsets, G).to(dtype).double(), rtol=2e-2,
                                atol=0.4)
     assert not dW[1].cpu().any()
+
+
+@pytest.mark.parametrize("fill", ["zeros", "ones", "random", "reuse"])
+def test_capi_paired_dw_dx_any_workspace_contents(lib, fill):
+    """The paired dW + dX call claims its dX tiles from counters in the
+    caller's workspace that carry a per-launch tag: whatever the workspace
+    held before (zeros, all-ones bytes, random bytes, the same workspace's
+    previous call), the results are the separate calls' bits."""
+    E, K, N, A = 8, 512, 2048, 8192
+    g = torch.Generator().manual_seed(41)
+    X = torch.randn(A, K, generator=g).to(torch.bfloat16).cuda()
+    W = (torch.randn(E, K, N, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    G = torch.randn(A, N, generator=g).to(torch.bfloat16).cuda()
+    off = torch.tensor([i * A // E for i in range(E + 1)], dtype=torch.int32, device="cuda")
+    dt = dtype_code(torch.bfloat16)
+    nb = lib.nt_grouped_gemm_workspace_bytes(dt, E, A, K, N)
+    s = current_stream()
+    dW_ref = torch.empty(E, K, N, dtype=torch.bfloat16, device="cuda")
+    dX_ref = torch.empty(A, K, dtype=torch.bfloat16, device="cuda")
+    w0 = torch.zeros(max(nb, 1), dtype=torch.uint8, device="cuda")
+    call("nt_grouped_gemm_dw", dt, ptr(X), ptr(off), ptr(G), E, A, K, N, ptr(dW_ref), ptr(w0), nb, s)
+    call("nt_grouped_gemm_dx", dt, ptr(W), ptr(off), ptr(G), E, A, K, N, ptr(dX_ref), None, 0, s)
+    w = ws(nb)
+    if fill == "zeros":
+        w.zero_()
+    elif fill == "ones":
+        w.fill_(0xFF)
+    else:
+        w.copy_(torch.randint(0, 256, (w.numel(),), generator=g, dtype=torch.uint8).cuda())
+    runs = 2 if fill == "reuse" else 1
+    for _ in range(runs):
+        dW = torch.full((E, K, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        dX = torch.full((A, K), float("nan"), dtype=torch.bfloat16, device="cuda")
+        call("nt_grouped_gemm_dw_dx", dt, ptr(X), ptr(W), ptr(off), ptr(G), E, A, K, N, ptr(dW),
+             ptr(dX), ptr(w), nb, s)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(dW), bits(dW_ref))
+        assert torch.equal(bits(dX), bits(dX_ref))
