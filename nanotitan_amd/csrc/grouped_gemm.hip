@@ -1420,20 +1420,23 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   }
 }
 
+// Every tile of a short-reduction GEMM takes the same time, so without a
+// delay all CUs reach their epilogues together and the chip writes in bursts
+// at HBM speed while the matrix cores wait. Half of each XCD's workgroups
+// (odd blockIdx / 8) start `ticks` late, a bounded wait on the constant
+// 100 MHz counter, and their stores then overlap the other half's main loops.
+__device__ __forceinline__ void stagger_wait(int32_t ticks) {
+  if (ticks > 0 && ((blockIdx.x / 8) & 1)) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)ticks) __builtin_amdgcn_s_sleep(8);
+  }
+}
+
 template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
           bool SPLIT>
 __global__ void __launch_bounds__(WGM * WGN * kWave)
 gg_mfma_kernel(GemmArgs g) {
-  if (g.stagger > 0 && ((blockIdx.x / 8) & 1)) {
-    // Every tile of a short-reduction GEMM takes the same time, so without
-    // this all CUs reach their epilogues together and the chip writes in
-    // bursts at HBM speed while the matrix cores wait. Half of each XCD's
-    // workgroups start one epilogue's write time late (a bounded wait on the
-    // constant 100 MHz counter), and their stores then overlap the other
-    // half's main loops.
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)g.stagger) __builtin_amdgcn_s_sleep(8);
-  }
+  stagger_wait(g.stagger);
   typedef GemmLds<T, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT> L;
   // [GELU table | stages]; the stages stay 1 KiB aligned.
   __shared__ __attribute__((aligned(1024))) char lds[L::kTabOff + L::kSmem];
@@ -1465,6 +1468,8 @@ gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, unsigned long long* dyn,
     gemm_tiles<T, kDw, 256, 256, 2, 4, 64, 2, kEpiPlain, false>(gw, blockIdx.x, nw, smem, s_pref,
                                                                s_gtab);
     __syncthreads();  // LDS is reused by the dX tiles below
+  } else {
+    stagger_wait(gx.stagger);  // of the workgroups that start on the dX
   }
   gemm_tiles<T, kDx, 256, 256, 2, 4, 64, 2, EPIX, SPLITX, true>(gx, blockIdx.x, gridDim.x, smem,
                                                               s_pref, s_gtab, dyn, &s_next, epoch);
@@ -1875,12 +1880,13 @@ int blocks_per_cu(K kernel, int threads) {
 }
 
 // Start delay (100 MHz ticks) for half the workgroups of a forward / dX
-// launch whose tiles are short (reduction <= 1024), many (at least 4 per CU)
-// and whose epilogue moves two or more tiles per output tile (outputs
-// written plus auxiliary tiles read): the time the whole chip needs to move
-// one round of that traffic at ~6 TB/s. Measured at C2's GELU up-projection,
-// warm and interleaved: 200-207 -> 185-195 us. Plain epilogues gained
-// nothing consistent (-3% to +2%), and at longer reductions or fewer tiles
+// launch whose tiles are short (reduction <= 1024) and many (at least 4 per
+// CU): the time the whole chip needs to move one round of the epilogue's
+// traffic (outputs written plus auxiliary tiles read) at ~6 TB/s. Measured
+// on C2's routed inputs, warm and interleaved, against no delay: GELU
+// up-projection 226 -> 200 us, plain up-projection 163 -> 149 us, plain dX
+// (reduction 512) 165 -> 152 us, GELU dX 199 -> 185 us. Half or 1.5 times
+// this delay gained less, 3 times lost; at longer reductions or fewer tiles
 // the delay only lengthens the tail.
 int32_t stagger_ticks(int mode, int epi, int64_t red, int64_t tiles, int64_t cus, int BM, int BN) {
   if (mode == kDw || red > 1024 || tiles < 4 * cus) return 0;
@@ -1888,7 +1894,6 @@ int32_t stagger_ticks(int mode, int epi, int64_t red, int64_t tiles, int64_t cus
   if (epi == kEpiGelu || epi == kEpiGeluGrad) tensors = 2;
   if (epi == kEpiSwiGLU) tensors = 3;
   if (epi == kEpiSwiGLUGrad) tensors = 4;
-  if (tensors < 2) return 0;
   const int64_t bytes = (int64_t)tensors * BM * (epi == kEpiSwiGLU ? BN / 2 : BN) * 2 * cus;
   return (int32_t)(bytes / 60000);  // bytes / 6 TB/s, in 10 ns ticks
 }
@@ -2409,6 +2414,8 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   const unsigned long long epoch = next_claim_epoch();
   plan_tiles<kDw>(gw, N, 256, 256);
   plan_tiles<kDx>(gx, K, 256, 256);
+  gx.stagger = stagger_ticks(kDx, EPIX, EPIX == kEpiDualK ? 2 * N : N,
+                             ceil_div(A, 256) * ceil_div(K, 256), cus, 256, 256);
   // split duties for the dX as launch_mfma_auto would choose them
   constexpr bool kPlain = EPIX == kEpiPlain || EPIX == kEpiDualK;
   const bool splitx = kPlain && (EPIX == kEpiDualK ? 2 * N : N) >= kSplitMinRed;
