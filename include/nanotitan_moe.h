@@ -236,7 +236,9 @@ int nt_route_topk_backward(const float* gates, const int32_t* topk, const float*
  * sizes (the forward and dX GEMMs need none; pass NULL, 0). It holds 256
  * bytes of tile counters (paired calls), then the fp32 partial sums of
  * experts whose reduction is split (skewed routing): at most 256 MiB plus
- * one K*N*4 slab; 256 bytes when no split can occur. A smaller or NULL
+ * one K*N*4 slab, and 8 bytes per slab and 256x256 dW tile of arrival
+ * counters (a paired call sums the partial sums in its own launch); 256
+ * bytes when no split can occur. A smaller or NULL
  * workspace is accepted: dW then runs unsplit (and unpaired). Its contents
  * need no initialisation: the counters carry a per-launch tag, and every
  * slab a launch reads it has written. Calls that overlap in time must not

@@ -432,6 +432,11 @@ struct GemmArgs {
   int32_t split_thr;  // dW: experts with more rows than this are split (when chunk > 0)
   int32_t slab_cap;   // dW: partial slabs the workspace holds (when chunk > 0)
   int32_t stagger;    // start delay of half the workgroups, 100 MHz ticks (0: none)
+  // Paired dW with split experts: arrival counters, one per (split expert,
+  // 256x256 output tile), tagged with done_epoch; the last chunk of a tile
+  // to arrive sums its slabs (fold_split_tile). Null: a reduce pass does.
+  unsigned long long* done;
+  unsigned long long done_epoch;
 };
 
 // Epilogues: plain store; forward GELU (out = gelu(h), out2 = gelu'(h), h
@@ -483,6 +488,9 @@ struct TileJobT {
   const U* pb2;    // SwiGLU forward: value weights; two-part dX: second W
   int64_t kred1;   // two-part dX: reduction length of the first part
   float* pf;       // dW of a split expert: fp32 partial slab origin (or null)
+  const float* pf0;  // split dW: the tile's origin in the expert's first slab
+  int32_t nch;       // split dW: the expert's reduction chunks
+  int64_t done_idx;  // split dW: the tile's arrival counter
 };
 typedef TileJobT<uint16_t> TileJob;
 
@@ -502,6 +510,9 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
   j.pb2 = nullptr;
   j.kred1 = 0;
   j.pf = nullptr;
+  j.pf0 = nullptr;
+  j.nch = 1;
+  j.done_idx = 0;
   int64_t mt;
   int nt;
   tile_coords(logical, mtiles, g.ntn, mt, nt);
@@ -534,7 +545,13 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
     const int64_t tile_off = (int64_t)mtl * BM * g.N + (int64_t)nt * BN;
     j.po = static_cast<U*>(g.out) + (int64_t)e * g.K * g.N + tile_off;
     j.ldo = g.N;
-    if (nch >= 2) j.pf = g.partial + (int64_t)(s_split[e] + c) * g.K * g.N + tile_off;
+    if (nch >= 2) {
+      j.pf = g.partial + (int64_t)(s_split[e] + c) * g.K * g.N + tile_off;
+      j.pf0 = g.partial + (int64_t)s_split[e] * g.K * g.N + tile_off;
+      j.nch = nch;
+      // s_split[e] is unique per split expert (they hold two or more slabs)
+      j.done_idx = ((int64_t)s_split[e] * g.ntm + mtl) * g.ntn + nt;
+    }
   } else {
     int e;
     int64_t r0, r1, mtl;
@@ -1139,6 +1156,45 @@ __device__ int64_t claim_tagged(unsigned long long* ctr, unsigned long long epoc
   return cnt < limit ? cnt : -1;
 }
 
+// Split dW tile of a paired launch, after its fp32 partial is stored: every
+// wave publishes its stores at agent scope (the slabs are read by a
+// workgroup on any XCD), then one thread counts the chunk on the tile's
+// counter. The last of the expert's nch chunks to arrive sums the nch slabs
+// in chunk order, the order and arithmetic of dw_reduce_kernel, and writes
+// the dW tile (8 columns per thread and step; K and N are multiples of 8).
+// `s_flag` is an LDS slot.
+template <typename T>
+__device__ void fold_split_tile(const GemmArgs& g, const TileJob& j, int64_t* s_flag) {
+  __threadfence();  // release this wave's partial stores
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *s_flag = claim_tagged(g.done + j.done_idx, g.done_epoch, j.nch) == j.nch - 1 ? 1 : 0;
+  __syncthreads();
+  if (*s_flag == 0) return;
+  __threadfence();  // acquire the other chunks' partials
+  const int64_t KN = g.K * g.N;
+  const int rows = (int)(j.rows_valid < 256 ? j.rows_valid : 256);
+  const int vecs = (int)((j.cols_valid < 256 ? j.cols_valid : 256) / 8);
+  typename elem<T>::storage* out = reinterpret_cast<typename elem<T>::storage*>(j.po);
+  for (int idx = threadIdx.x; idx < rows * vecs; idx += blockDim.x) {
+    const int m = idx / vecs, n = (idx % vecs) * 8;
+    const float* src = j.pf0 + (int64_t)m * g.N + n;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < j.nch; ++c) {
+      const float4 u = *reinterpret_cast<const float4*>(src + (int64_t)c * KN);
+      const float4 v = *reinterpret_cast<const float4*>(src + (int64_t)c * KN + 4);
+      acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
+      acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
+    }
+    uint4 r;
+    r.x = (uint32_t)elem<T>::store(acc[0]) | ((uint32_t)elem<T>::store(acc[1]) << 16);
+    r.y = (uint32_t)elem<T>::store(acc[2]) | ((uint32_t)elem<T>::store(acc[3]) << 16);
+    r.z = (uint32_t)elem<T>::store(acc[4]) | ((uint32_t)elem<T>::store(acc[5]) << 16);
+    r.w = (uint32_t)elem<T>::store(acc[6]) | ((uint32_t)elem<T>::store(acc[7]) << 16);
+    *reinterpret_cast<uint4*>(out + (int64_t)m * j.ldo + n) = r;
+  }
+}
+
 // The tile loop of workgroup `wg` of `G` that share this GEMM (the kernel's
 // body; gg_pair_kernel runs two of them side by side).
 template <typename T, int MODE, int BM, int BN, int WGM, int WGN, int BK, int NS, int EPI,
@@ -1366,6 +1422,12 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
     stores_out = false;
     if (MODE == kDw && job.pf != nullptr) {
       store_partial(acc, job, wm * WM, wn * WN, lane);
+      if (g.done != nullptr) {
+        // the fold's fields are set up again here, not kept live across the k-loop
+        TileJob fj;
+        setup_job<MODE, BM, BN, EPI>(g, s_pref, mtiles, logical, fj);
+        fold_split_tile<T>(g, fj, s_next);
+      }
     } else if constexpr (kDual == 1) {
       // gate and value rounded as the unfused GEMMs would store them, then
       // hidden = round(round(silu(gate)) * value); three LDS-staged stores.
@@ -1466,7 +1528,7 @@ gg_pair_kernel(GemmArgs gw, GemmArgs gx, int32_t nw, unsigned long long* dyn,
   __shared__ int64_t s_next;
   if ((int32_t)blockIdx.x < nw) {
     gemm_tiles<T, kDw, 256, 256, 2, 4, 64, 2, kEpiPlain, false>(gw, blockIdx.x, nw, smem, s_pref,
-                                                               s_gtab);
+                                                               s_gtab, nullptr, &s_next);
     __syncthreads();  // LDS is reused by the dX tiles below
   } else {
     stagger_wait(gx.stagger);  // of the workgroups that start on the dX
@@ -2163,11 +2225,14 @@ bool dw_big_tiles(int64_t A, int64_t K, int64_t N, int32_t E, hipStream_t s) {
   return chunks * ceil_div(K, 256) * ceil_div(N, 256) * 2 >= device_cus(s) * 3;
 }
 
-// Workspace of the dW entry points: kCtrBytes of tile counters (paired
-// launches), then the fp32 partial slabs of split experts.
+// Workspace of the dW entry points: kCtrBytes of tile-claim counters
+// (paired launches), the fp32 partial slabs of split experts, then the
+// paired launch's arrival counters of their 256x256 tiles (fold_split_tile),
+// indexed by the expert's first slab.
 constexpr size_t kCtrBytes = 256;
 size_t dw_ws_bytes(int64_t A, int64_t K, int64_t N, int32_t E) {
-  return (size_t)dw_slabs(A, dw_split(A, K, N, E)) * (size_t)(K * N * 4);
+  const size_t slabs = (size_t)dw_slabs(A, dw_split(A, K, N, E));
+  return slabs * (size_t)(K * N * 4) + slabs * (size_t)(ceil_div(K, 256) * ceil_div(N, 256) * 8);
 }
 
 // fp32 MFMA kernel: 16-byte aligned operands and outputs, K and N multiples
@@ -2404,14 +2469,17 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
   }
   GemmArgs gw{X, dOut, offsets, E, A, K, N, dW, 0, 0, 0, nullptr, nullptr, 0, nullptr};
   float* partial = split ? reinterpret_cast<float*>(static_cast<char*>(ws) + kCtrBytes) : nullptr;
+  unsigned long long* dyn = static_cast<unsigned long long*>(ws);
+  const unsigned long long epoch = next_claim_epoch();
   if (split) {
     gw.chunk = sp.R;
     gw.split_thr = sp.thr;
     gw.slab_cap = (int32_t)dw_slabs(A, sp);
     gw.partial = partial;
+    // the split tiles sum their slabs in the launch (no reduce pass)
+    gw.done = reinterpret_cast<unsigned long long*>(partial + dw_slabs(A, sp) * K * N);
+    gw.done_epoch = epoch;
   }
-  unsigned long long* dyn = static_cast<unsigned long long*>(ws);
-  const unsigned long long epoch = next_claim_epoch();
   plan_tiles<kDw>(gw, N, 256, 256);
   plan_tiles<kDx>(gx, K, 256, 256);
   gx.stagger = stagger_ticks(kDx, EPIX, EPIX == kEpiDualK ? 2 * N : N,
@@ -2437,9 +2505,7 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
       hipLaunchKernelGGL((gg_pair_kernel<f16, EPIX, false>), grid, block, 0, stream, gw, gx, nw32, dyn, epoch);
     }
   }
-  int st = launch_status();
-  if (st != NT_OK || !split) return st;
-  return launch_dw_reduce(dtype, offsets, E, A, K, N, sp, partial, dW, stream);
+  return launch_status();
 }
 
 }  // namespace

@@ -266,11 +266,14 @@ def test_split_duty_tiles_ragged(ext, dtype, K, N):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("counts,K,N", [([7680] * 8, 2048, 512), ([7680] * 8, 512, 2048),
                                         ([20000, 0, 3, 9000, 5000], 1024, 256),
+                                        ([12000, 11000, 40, 9000], 520, 264),
                                         ([5, 0, 17], 64, 128)])
 def test_paired_dw_dx_matches_separate_calls(ext, dtype, counts, K, N):
     """bwd_grouped_gemm_dW_dX[_gelu]: the dW runs beside the dX in one
-    launch when it has few 256x256 tiles (the first three cases; the third
-    also splits its head expert's reduction), else after it. Outputs equal
+    launch when it has few 256x256 tiles (the first four cases), else after
+    it. The third splits its head expert's reduction, the fourth three
+    experts, on tiles cut by K and N; the paired launch sums their partial
+    slabs itself, in the order of the separate reduce pass. Outputs equal
     the separate calls bit for bit, and work queued next on the current
     stream sees them complete."""
     g = torch.Generator().manual_seed(K + N + len(counts))
