@@ -123,7 +123,7 @@ def make_workload(cfg_id: int, device: str, seed: int = SEED, draw: str = "cpu")
 # [T,d]; combine backward reads dY once and the packed rows, writes dy and
 # dw; pack backward reads the packed grads, gate grads and inverse map and
 # writes dX and dw.
-def hbm_bytes(kind, T, d, A, b, b_out=None, b_grad=None):
+def hbm_bytes(kind, T, d, A, b, b_out=None, b_grad=None, E=None):
     if kind == "dispatch":
         return T * d * b + A * d * b + 8.0 * A + 12.0 * A
     if kind == "combine_fwd":
@@ -132,6 +132,8 @@ def hbm_bytes(kind, T, d, A, b, b_out=None, b_grad=None):
         return T * d * (b if b_grad is None else b_grad) + 2.0 * A * d * b + 12.0 * A
     if kind == "pack_bwd":
         return A * d * b + T * d * b + 12.0 * A
+    if kind == "pack_bwd_route":  # no dw; reads gates and ids, writes dlogits [T,E] f32
+        return A * d * b + T * d * b + 16.0 * A + 4.0 * T * E
     raise ValueError(kind)
 
 
@@ -156,6 +158,7 @@ class LaunchTimer:
         "combine_inv": "combine_fwd",
         "combine_backward_inv": "combine_bwd",
         "pack_backward_inv": "pack_bwd",
+        "pack_backward_inv_route": "pack_bwd",
     }
 
     def __init__(self, ext):
@@ -239,6 +242,10 @@ class LaunchTimer:
             dpX, _dpw, inv = args
             return hbm_bytes("pack_bwd", inv.shape[0], dpX.shape[1], dpX.shape[0],
                              dpX.element_size())
+        if name == "pack_backward_inv_route":
+            dpX, _dpw, inv, _gates, _topk, E = args
+            return hbm_bytes("pack_bwd_route", inv.shape[0], dpX.shape[1], dpX.shape[0],
+                             dpX.element_size(), E=E)
         return 0.0
 
     def summary(self):

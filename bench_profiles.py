@@ -126,7 +126,8 @@ def algorithmic(cfg_id: int):
         "combine_bwd": T * d * b + 2 * A * d * b + 12 * A,
         "combine_fwd": A * d * b + 8 * A + T * d * b,
         "dispatch_pack": T * d * b + A * d * b + 20 * A,
-        "pack_bwd": A * d * b + T * d * b + 12 * A,
+        # the layer's launches also write the router's gradient (no dw)
+        "pack_bwd": A * d * b + T * d * b + 16 * A + 4 * T * E,
         "gemm_fwd_gelu": (A * d + E * d * f + 2 * A * f) * b,
         "gemm_fwd": (A * f + E * f * d + A * d) * b,
         "gemm_pair_dw_dx_gelu": (3 * A * f + A * d + 2 * E * f * d) * b,

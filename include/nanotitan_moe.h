@@ -202,6 +202,20 @@ int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int
                          int64_t T, int32_t k, int64_t d, void* dX, float* dw,
                          hipStream_t stream);
 
+/* nt_pack_backward_inv followed by nt_route_topk_backward on its dw, in one
+ * launch when k <= 8: dX as nt_pack_backward_inv, and dlogits [T,E] f32 the
+ * router gradient for gates [T,k], topk [T,k] and dgates dw (bit-identical
+ * to the two calls). dw [T,k] is optional (NULL: not written) when k <= 8
+ * and required above (the two launches then run). Replaces the pack
+ * backward (reference csrc/kernels/backward_pack_kernel.cu:10-44) and the
+ * backward of the router's softmax / top-k / renormalisation, which the
+ * reference leaves to torch autograd (src/model/cuda_backend.py:30-37),
+ * for a layer whose gates feed only the dispatch. */
+int nt_pack_backward_inv_route(int dtype, const void* dpX, const float* dpw, const int32_t* inv,
+                               const float* gates, const int32_t* topk, int64_t T, int32_t k,
+                               int64_t d, int32_t E, void* dX, float* dlogits, float* dw,
+                               hipStream_t stream);
+
 /* -------------------------------------------------------------------- router */
 
 /* Router gate for logits [T,E] f32: top-k experts by logit (ties to the

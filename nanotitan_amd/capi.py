@@ -83,6 +83,10 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_int, _P, _P, _P, c_int64, c_int32, c_int64, _P, _P, _P],
     ),
+    "nt_pack_backward_inv_route": (
+        c_int,
+        [c_int, _P, _P, _P, _P, _P, c_int64, c_int32, c_int64, c_int32, _P, _P, _P, _P],
+    ),
     "nt_route_topk": (c_int, [_P, c_int64, c_int32, c_int32, _P, _P, _P, _P]),
     "nt_route_topk_count": (
         c_int,

@@ -635,15 +635,56 @@ pack_bwd_kernel(const typename elem<T>::storage* __restrict__ dpX, const float* 
   }
 }
 
+// The router's backward fused into the inverse-map pack backward (a null
+// dlogits: none). For token t with gates g_j = gates[t,k+j], experts
+// topk[t,j] and gate gradients dg_j = dpw[inv[t,j]] (0 when inv < 0),
+// dlogits[t,:] is zero except at the selected experts, where it is
+// g_j (dg_j - sum_i dg_i g_i): the arithmetic and order of
+// route_topk_backward_kernel, so the result is the two-launch one bit for bit.
+struct RouteGrad {
+  const float* gates;
+  const int32_t* topk;
+  int32_t E;
+  float* dlogits;
+};
+// Wave-wide (every lane calls it): lane `sl` of the `seg` lanes serving
+// token t (sl < k) holds slot sl's gate gradient `dg`; the slots' gates and
+// experts are read once per lane and broadcast by shuffles, so each token
+// costs one round of loads. Lane sl writes experts sl, sl+seg, ... (live:
+// t is a token).
+__device__ __forceinline__ void route_grad_row(const RouteGrad& rg, int64_t t, bool live, int32_t k,
+                                               int sl, int seg, float dg) {
+  float g = 0.f;
+  int32_t ej = -1;
+  if (live && sl < k) {
+    g = rg.gates[t * k + sl];
+    ej = rg.topk[t * k + sl];
+  }
+  const int sb = lane_id() - sl;  // the segment's first lane
+  float part = 0.f;
+  for (int j = 0; j < k; ++j) part += __shfl(dg, sb + j, kWave) * __shfl(g, sb + j, kWave);
+  for (int e0 = 0; e0 < rg.E; e0 += seg) {
+    const int e = e0 + sl;
+    float out = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int32_t ejj = __shfl(ej, sb + j, kWave);
+      const float gj = __shfl(g, sb + j, kWave), dgj = __shfl(dg, sb + j, kWave);
+      if (ejj == e) out += gj * (dgj - part);
+    }
+    if (live && e < rg.E) rg.dlogits[t * rg.E + e] = out;
+  }
+}
+
 // Inverse-map pack backward for small fan-in: same sums as pack_bwd_kernel
 // (ascending packed order, fp32), U tokens per wave with every row load
-// issued up front.
+// issued up front. dw may be null (not written); rg.dlogits non-null adds
+// the router's backward (route_grad_row).
 template <typename T, int VE, int KMAX, int U, bool RAW>
 __global__ void __launch_bounds__(kThreads)
 pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
                     const float* __restrict__ dpw, const int32_t* __restrict__ inv,
                     int64_t T_, int32_t k, int64_t d, typename elem<T>::storage* __restrict__ dX,
-                    float* __restrict__ dw) {
+                    float* __restrict__ dw, RouteGrad rg) {
   constexpr int kSeg = kWave / U;
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
@@ -656,7 +697,9 @@ pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
   {
     const int64_t tl = t0 + lane / kSeg;
     const int jl = lane % kSeg;
-    if (jl < k && tl < T_) dw[tl * k + jl] = (mine >= 0 && mine < rows) ? dpw[mine] : 0.f;
+    const float dg = (jl < k && tl < T_ && mine >= 0 && mine < rows) ? dpw[mine] : 0.f;
+    if (dw != nullptr && jl < k && tl < T_) dw[tl * k + jl] = dg;
+    if (rg.dlogits != nullptr) route_grad_row(rg, tl, tl < T_, k, jl, kSeg, dg);
   }
   for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
     RowBuf<T, VE, RAW> x[U][KMAX];
@@ -830,7 +873,7 @@ int run_combine_bwd_inv(const void* y, const int32_t* inv, const float* w, const
 template <typename T>
 int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* expert,
                  const int32_t* topk, int64_t T_, int32_t k, int64_t d, void* dX, float* dw,
-                 hipStream_t s) {
+                 hipStream_t s, RouteGrad rg) {
   if (T_ == 0) return NT_OK;
   using S = typename elem<T>::storage;
   const dim3 grid((unsigned)ceil_div(T_, kWaves));
@@ -840,7 +883,7 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   if (src.start == nullptr && expert == nullptr && k <= 8) {
     const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
 #define NT_PBI_U(VE, KM, U, RAW) \
-  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U), RAW>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw)
+  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U), RAW>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw, rg)
 #define NT_PBI(VE, KM)                                                    \
   do {                                                                    \
     if (long_rows && KM <= 2) NT_PBI_U(VE, KM, kPackBwdULong, false);     \
@@ -873,14 +916,16 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   return launch_status();
 }
 
+// rg.dlogits non-null: the inverse-map kernel (src.start null, no expert
+// array, k <= 8) also writes the router's gradient; the caller ensures that.
 int pack_bwd_dispatch(int dtype, const void* dpX, const float* dpw, ListSrc src,
                       const int32_t* expert, const int32_t* topk, int64_t T_, int32_t k,
-                      int64_t d, void* dX, float* dw, hipStream_t s) {
+                      int64_t d, void* dX, float* dw, hipStream_t s, RouteGrad rg = RouteGrad{}) {
   switch (dtype) {
-    case NT_F32: return run_pack_bwd<float>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
-    case NT_F64: return run_pack_bwd<double>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
-    case NT_F16: return run_pack_bwd<f16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
-    case NT_BF16: return run_pack_bwd<bf16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s);
+    case NT_F32: return run_pack_bwd<float>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s, rg);
+    case NT_F64: return run_pack_bwd<double>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s, rg);
+    case NT_F16: return run_pack_bwd<f16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s, rg);
+    case NT_BF16: return run_pack_bwd<bf16>(dpX, dpw, src, expert, topk, T_, k, d, dX, dw, s, rg);
     default: return NT_ERR_DTYPE;
   }
 }
@@ -1002,6 +1047,28 @@ int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int
     return NT_ERR_INVALID_ARG;
   ListSrc src{nullptr, inv, k, T * k};
   return pack_bwd_dispatch(dtype, dpX, dpw, src, nullptr, nullptr, T, k, d, dX, dw, stream);
+}
+
+int nt_pack_backward_inv_route(int dtype, const void* dpX, const float* dpw, const int32_t* inv,
+                               const float* gates, const int32_t* topk, int64_t T, int32_t k,
+                               int64_t d, int32_t E, void* dX, float* dlogits, float* dw,
+                               hipStream_t stream) {
+  if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
+  if (!sizes_ok(T, k, d) || k < 1 || E < 1 || E > NT_MAX_EXPERTS) return NT_ERR_INVALID_ARG;
+  if (T * (int64_t)k > INT32_MAX || T * (int64_t)E > INT32_MAX) return NT_ERR_TOO_LARGE;
+  if (T > 0 && (inv == nullptr || dpw == nullptr || gates == nullptr || topk == nullptr ||
+                dlogits == nullptr || (d > 0 && (dpX == nullptr || dX == nullptr))))
+    return NT_ERR_INVALID_ARG;
+  ListSrc src{nullptr, inv, k, T * k};
+  if (k <= 8) {
+    const RouteGrad rg{gates, topk, E, dlogits};
+    return pack_bwd_dispatch(dtype, dpX, dpw, src, nullptr, nullptr, T, k, d, dX, dw, stream, rg);
+  }
+  // More slots than the inverse-map kernel takes: the two launches it fuses.
+  if (T > 0 && dw == nullptr) return NT_ERR_INVALID_ARG;
+  const int st = pack_bwd_dispatch(dtype, dpX, dpw, src, nullptr, nullptr, T, k, d, dX, dw, stream);
+  if (st != NT_OK) return st;
+  return nt_route_topk_backward(gates, topk, dw, T, E, k, dlogits, stream);
 }
 
 }  // extern "C"

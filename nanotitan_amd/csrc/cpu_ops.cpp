@@ -624,6 +624,16 @@ Tensor route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int64_t num
   return dl;
 }
 
+// The pack backward whose dw is the router's gate gradient, then the router
+// backward on it (the two ops above, in sequence).
+std::tuple<Tensor, Tensor> pack_backward_inv_route(Tensor dpX, Tensor dpw, Tensor inv, Tensor gates,
+                                                   Tensor topk, int64_t num_experts) {
+  TORCH_CHECK(gates.sizes() == inv.sizes() && topk.sizes() == inv.sizes(),
+              "gates and topk must be [T,k] like inv");
+  auto [dX, dw] = pack_backward_inv(dpX, dpw, inv);
+  return {dX, route_topk_backward(gates, topk, dw, num_experts)};
+}
+
 // --------------------------------------------------------- grouped GEMM
 //
 // Per expert segment: fp32 (fp64 for float64) products of the rows, one
@@ -834,4 +844,5 @@ TORCH_LIBRARY_IMPL(nanotitan, CPU, m) {
   m.impl("combine_inv", &combine_inv);
   m.impl("combine_backward_inv", &combine_backward_inv);
   m.impl("pack_backward_inv", &pack_backward_inv);
+  m.impl("pack_backward_inv_route", &pack_backward_inv_route);
 }

@@ -720,6 +720,40 @@ std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv)
   return {dX, dw};
 }
 
+// pack_backward_inv whose dw feeds route_topk_backward, fused: (dX [T,d],
+// dlogits [T,E]).
+std::tuple<Tensor, Tensor> pack_backward_inv_route(Tensor dpX, Tensor dpw, Tensor inv, Tensor gates,
+                                                   Tensor topk, int64_t num_experts) {
+  TORCH_CHECK(dpX.is_contiguous() && dpw.is_contiguous() && inv.is_contiguous() &&
+                  gates.is_contiguous() && topk.is_contiguous(),
+              "inputs must be contiguous");
+  check_device(dpX, "packed_X_grad");
+  check_f32(dpw, "packed_topk_weights_grad");
+  check_i32(inv, "inv");
+  check_f32(gates, "gates");
+  check_i32(topk, "topk");
+  TORCH_CHECK(dpX.dim() == 2 && inv.dim() == 2, "expected packed_X_grad [A,d], inv [T,k]");
+  TORCH_CHECK(dpX.size(0) == inv.numel() && dpw.numel() == inv.numel(),
+              "packed_X_grad and packed_topk_weights_grad must have T*k = inv.numel() rows");
+  TORCH_CHECK(gates.sizes() == inv.sizes() && topk.sizes() == inv.sizes(),
+              "gates and topk must be [T,k] like inv");
+  TORCH_CHECK(num_experts >= 1 && num_experts <= NT_MAX_EXPERTS, "num_experts out of range");
+  check_same_device(dpX, {&dpw, &inv, &gates, &topk});
+  const int64_t T = inv.size(0), k = inv.size(1), d = dpX.size(1);
+  c10::hip::HIPGuard guard(dpX.get_device());
+  Tensor dX = at::empty({T, d}, dpX.options());
+  Tensor dlogits = at::empty({T, num_experts}, gates.options());
+  // The fused kernel takes k <= 8; above, the two launches need dw.
+  Tensor dw = k > 8 ? at::empty({T, k}, dpw.options()) : Tensor();
+  check_status(nt_pack_backward_inv_route(
+                   dtype_code(dpX), dpX.data_ptr(), dpw.data_ptr<float>(),
+                   inv.data_ptr<int32_t>(), gates.data_ptr<float>(), topk.data_ptr<int32_t>(), T,
+                   (int32_t)k, d, (int32_t)num_experts, dX.data_ptr(), dlogits.data_ptr<float>(),
+                   k > 8 ? dw.data_ptr<float>() : nullptr, stream_of(dpX)),
+               "pack_backward_inv_route");
+  return {dX, dlogits};
+}
+
 // stream_copy(dst, src, blocks=0): the library's 16-byte streaming copy of
 // src's bytes into dst (the achievable-bandwidth reference of the benchmark).
 void stream_copy(Tensor dst, Tensor src, int64_t blocks) {
@@ -875,6 +909,12 @@ std::tuple<Tensor, Tensor> pack_backward_inv(Tensor dpX, Tensor dpw, Tensor inv)
           at::empty({inv.size(0), inv.size(1)}, dpw.options())};
 }
 
+std::tuple<Tensor, Tensor> pack_backward_inv_route(Tensor dpX, Tensor dpw, Tensor inv, Tensor gates,
+                                                   Tensor topk, int64_t num_experts) {
+  return {at::empty({inv.size(0), dpX.size(1)}, dpX.options()),
+          at::empty({inv.size(0), num_experts}, gates.options())};
+}
+
 }  // namespace meta
 
 }  // namespace
@@ -932,6 +972,8 @@ TORCH_LIBRARY(nanotitan, m) {
         "Tensor grad) -> (Tensor, Tensor)");
   m.def("pack_backward_inv(Tensor packed_X_grad, Tensor packed_topk_weights_grad, Tensor inv) "
         "-> (Tensor, Tensor)");
+  m.def("pack_backward_inv_route(Tensor packed_X_grad, Tensor packed_topk_weights_grad, "
+        "Tensor inv, Tensor gates, Tensor topk, int num_experts) -> (Tensor, Tensor)");
 }
 
 #define NT_IMPL_ALL(m, NS)                                                  \
@@ -960,7 +1002,8 @@ TORCH_LIBRARY(nanotitan, m) {
   m.impl("pack_tokens_inv", &NS pack_tokens_inv);                           \
   m.impl("combine_inv", &NS combine_inv);                                   \
   m.impl("combine_backward_inv", &NS combine_backward_inv);                 \
-  m.impl("pack_backward_inv", &NS pack_backward_inv)
+  m.impl("pack_backward_inv", &NS pack_backward_inv);                       \
+  m.impl("pack_backward_inv_route", &NS pack_backward_inv_route)
 
 TORCH_LIBRARY_IMPL(nanotitan, CUDA, m) { NT_IMPL_ALL(m, ); }
 
@@ -1001,6 +1044,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("combine_inv", &combine_inv, "Combine driven by the inverse map");
   m.def("combine_backward_inv", &combine_backward_inv, "Combine backward driven by the inverse map");
   m.def("pack_backward_inv", &pack_backward_inv, "Pack backward driven by the inverse map");
+  m.def("pack_backward_inv_route", &pack_backward_inv_route,
+        "pack_backward_inv with the router's backward on its dw -> (X_grad, dlogits)");
   m.def("route_topk", &route_topk, "Fused softmax / top-k / renorm router gate -> (gates, topk)");
   m.def("bwd_grouped_gemm_dW_dX", &bwd_grouped_gemm_dW_dX,
         "dW and dX of one projection in one call (a dW with few tiles runs beside the dX)");

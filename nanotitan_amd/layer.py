@@ -30,9 +30,8 @@ from torch.profiler import record_function
 
 from nanotitan_amd.moe_ops import (
     combine_inv_fn,
-    dispatch_fn,
     grouped_gelu_ffn_fn,
-    route_count_fn,
+    route_dispatch_fn,
     route_fn,
     swiglu_ffn_fn,
 )
@@ -141,12 +140,11 @@ def moe_forward_from_logits(x_flat, logits, experts, num_experts, top_k):
     Returns (out [T,d], counts [E], gates [T,k]).
     """
     # The router kernel also counts the tokens per expert and per dispatch
-    # block, so the dispatch starts at its scan.
-    with record_function("moe/topK"):
-        gates, idx, counted = route_count_fn(logits.float().contiguous(), top_k, x_flat)
-    with record_function("moe/pack_tokens"):
-        packed_X, packed_w, counts, offsets, _token_id, inv = dispatch_fn(
-            x_flat, gates, idx, num_experts, counted
+    # block, so the dispatch starts at its scan; in the backward, the pack
+    # backward also writes the router's gradient.
+    with record_function("moe/topK_pack_tokens"):
+        gates, idx, packed_X, packed_w, counts, offsets, _token_id, inv = route_dispatch_fn(
+            logits.float().contiguous(), top_k, x_flat, num_experts
         )
     with record_function("moe/expert_compute"):
         y = experts(packed_X, offsets)

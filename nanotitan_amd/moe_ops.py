@@ -363,12 +363,60 @@ class RouteCountFN(torch.autograd.Function):
                                        ctx.num_experts), None, None
 
 
+class RouteDispatchFN(torch.autograd.Function):
+    """Router gate (with the dispatch's count) and dispatch in one Function.
+
+    Forward: route_topk_count on logits [T,E] f32, then dispatch_tokens_counted
+    of X with those gates. Returns (gates, topk, packed_X, packed_w, counts,
+    offsets, token_id, inv), the outputs of RouteCountFN and DispatchFN.
+    Backward: when the gates get no gradient of their own (they feed only the
+    dispatch), one launch writes dX and dlogits (pack_backward_inv_route);
+    otherwise the pack backward's gate gradient is added to theirs before the
+    router's backward. Either way the result equals RouteCountFN followed by
+    DispatchFN.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, top_k, X, num_experts):
+        ext = get_hip_extension()
+        gates, topk, ws = ext.route_topk_count(logits.contiguous(), top_k, X)
+        outs = ext.dispatch_tokens_counted(X, gates, topk, num_experts, ws)
+        counts, offsets, packed_X, token_id, _expert, packed_w, inv = outs
+        ctx.save_for_backward(gates, topk, inv)
+        ctx.num_experts = logits.shape[1]
+        ctx.mark_non_differentiable(topk, counts, offsets, token_id, inv)
+        ctx.set_materialize_grads(False)
+        return gates, topk, packed_X, packed_w, counts, offsets, token_id, inv
+
+    @staticmethod
+    def backward(ctx, dgates, _dtopk, packed_X_grad, packed_w_grad, *_):
+        ext = get_hip_extension()
+        gates, topk, inv = ctx.saved_tensors
+        if packed_X_grad is None:
+            raise RuntimeError("route_dispatch_fn backward needs a gradient for packed_X")
+        if packed_w_grad is None:
+            packed_w_grad = torch.zeros(inv.numel(), dtype=torch.float32, device=inv.device)
+        dpX, dpw = packed_X_grad.contiguous(), packed_w_grad.contiguous()
+        if dgates is None:
+            X_grad, dlogits = ext.pack_backward_inv_route(dpX, dpw, inv, gates, topk,
+                                                          ctx.num_experts)
+        else:
+            X_grad, w_grad = ext.pack_backward_inv(dpX, dpw, inv)
+            dlogits = ext.route_topk_backward(gates, topk, (w_grad + dgates.float()).contiguous(),
+                                              ctx.num_experts)
+        return dlogits, None, X_grad, None
+
+
 def route_fn(logits, top_k):
     return RouteFN.apply(logits, top_k)
 
 
 def route_count_fn(logits, top_k, X):
     return RouteCountFN.apply(logits, top_k, X)
+
+
+def route_dispatch_fn(logits, top_k, X, num_experts):
+    return RouteDispatchFN.apply(logits, top_k, X, num_experts)
 
 
 def dispatch_fn(X, topk_weights, topk_experts, num_experts, counted_ws=None):

@@ -203,6 +203,34 @@ def test_inverse_map_kernels_with_dropped_slots(ext, k, dtype):
     assert torch.equal(bits(dw2), bits(torch.from_numpy(want_dw2)))
 
 
+@pytest.mark.parametrize("k,E,d,dtype", [(1, 4, 40, torch.bfloat16), (2, 8, 512, torch.bfloat16),
+                                         (5, 17, 40, torch.float32), (8, 64, 512, torch.bfloat16),
+                                         (8, 128, 2048, torch.float16), (12, 40, 64, torch.bfloat16)])
+def test_pack_backward_inv_route_equals_the_two_ops(ext, k, E, d, dtype):
+    """pack_backward_inv_route: the pack backward and the router's backward
+    on its dw, in one launch (k <= 8) or two (k = 12). Bit-equal to
+    pack_backward_inv followed by route_topk_backward, with gates and ids from
+    the router on random logits and an inverse map with dropped (-1) and
+    out-of-range slots in random packed order."""
+    T = 1501
+    A = T * k
+    g = torch.Generator().manual_seed(7 * k + E)
+    gates, topk = ext.route_topk(torch.randn(T, E, generator=g).cuda(), k)
+    inv = torch.randperm(A, generator=g).to(torch.int32).view(T, k).clone()
+    inv[torch.rand(T, k, generator=g) < 0.05] = -1
+    inv[torch.rand(T, k, generator=g) < 0.02] = A + 3
+    inv = inv.cuda()
+    dpX = torch.randn(A, d, generator=g).to(dtype).cuda()
+    dpw = torch.randn(A, generator=g).cuda()
+    dX_ref, dw_ref = ext.pack_backward_inv(dpX, dpw, inv)
+    dl_ref = ext.route_topk_backward(gates, topk, dw_ref, E)
+    dX, dl = ext.pack_backward_inv_route(dpX, dpw, inv, gates, topk, E)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(dX), bits(dX_ref))
+    assert torch.equal(bits(dl), bits(dl_ref))
+    assert (dl != 0).sum(1).max().item() <= k
+
+
 def test_inverse_map_ops_check_row_counts(ext):
     """The inverse-map ops read rows p < T*k of their packed inputs: a tensor
     with another row count is rejected before any launch."""

@@ -21,7 +21,7 @@ LAYER_OPS = ["grouped_gemm_gelu", "bwd_grouped_gemm_dX_gelu", "grouped_gemm_swig
              "bwd_grouped_gemm_dW_dX_gelu", "bwd_grouped_gemm_dW_dX_swiglu",
              "bwd_grouped_gemm_dW_dX2", "route_topk", "route_topk_count", "route_topk_backward",
              "dispatch_tokens", "dispatch_tokens_counted", "pack_tokens_inv", "combine_inv",
-             "combine_backward_inv", "pack_backward_inv"]
+             "combine_backward_inv", "pack_backward_inv", "pack_backward_inv_route"]
 DTYPES = [torch.float32, torch.float16, torch.bfloat16, torch.float64]
 
 
@@ -168,6 +168,11 @@ def test_inverse_map_ops_and_pack_backward(ops, dtype, T, k, E, d):
     assert torch.equal(bits(dX), bits(want_dX)) and torch.equal(bits(dw2), bits(torch.from_numpy(want_dw2)))
     dX2, dw3 = ops.pack_backward_inv(dpX, dpw, inv)
     assert torch.equal(bits(dX2), bits(want_dX)) and torch.equal(bits(dw3), bits(torch.from_numpy(want_dw2)))
+    # the router's backward on that dw, fused (route_topk_backward is pinned
+    # against torch autograd in test_route_topk_vs_oracle)
+    dX3, dl = ops.pack_backward_inv_route(dpX, dpw, inv, w, topk, E)
+    assert torch.equal(bits(dX3), bits(want_dX))
+    assert torch.equal(bits(dl), bits(ops.route_topk_backward(w, topk, dw3, E)))
 
 
 def test_pack_backward_first_match_rule(ops):
@@ -323,6 +328,7 @@ def _cases():
         "combine_inv": (pX, inv, pw, torch.bfloat16),
         "combine_backward_inv": (pX, inv, pw, dYt),
         "pack_backward_inv": (pX, pw, inv),
+        "pack_backward_inv_route": (pX, pw, inv, w, topk, E),
     }
 
 
