@@ -1165,13 +1165,19 @@ __device__ int64_t claim_tagged(unsigned long long* ctr, unsigned long long epoc
 // `s_flag` is an LDS slot.
 template <typename T>
 __device__ void fold_split_tile(const GemmArgs& g, const TileJob& j, int64_t* s_flag) {
-  __threadfence();  // release this wave's partial stores
+  __threadfence();  // this wave's partial stores complete and written back
   __syncthreads();
-  if (threadIdx.x == 0)
-    *s_flag = claim_tagged(g.done + j.done_idx, g.done_epoch, j.nch) == j.nch - 1 ? 1 : 0;
+  if (threadIdx.x == 0) {
+    // release (after the barrier: every wave's stores), count, and on the
+    // last arrival acquire, before the flag hands the slabs to every wave
+    __threadfence();
+    const bool last = claim_tagged(g.done + j.done_idx, g.done_epoch, j.nch) == j.nch - 1;
+    if (last) __threadfence();
+    *s_flag = last ? 1 : 0;
+  }
   __syncthreads();
   if (*s_flag == 0) return;
-  __threadfence();  // acquire the other chunks' partials
+  __threadfence();  // acquire in every wave that reads the other chunks' partials
   const int64_t KN = g.K * g.N;
   const int rows = (int)(j.rows_valid < 256 ? j.rows_valid : 256);
   const int vecs = (int)((j.cols_valid < 256 ? j.cols_valid : 256) / 8);
