@@ -254,3 +254,45 @@ def test_moe_module_matches_reference_dataflow(ext):
     _close_rms(moe.experts.W_gate.grad, Wg.grad, rtol=5e-2)
     _close_rms(moe.experts.W_val.grad, Wv.grad, rtol=5e-2)
     _close_rms(moe.experts.W_out.grad, Wo.grad, rtol=5e-2)
+
+
+@pytest.mark.parametrize("E,k,d,dtype", [(8, 2, 512, torch.bfloat16), (64, 8, 64, torch.float16),
+                                         (40, 12, 32, torch.float32)])
+@pytest.mark.parametrize("gates_used", [False, True])
+def test_route_dispatch_fn_matches_separate_functions(ext, E, k, d, dtype, gates_used):
+    """route_dispatch_fn (router + dispatch in one Function, its backward
+    fused into the pack backward) against route_count_fn followed by
+    dispatch_fn: the same forward outputs, and bit-equal X and logits
+    gradients. gates_used: the loss also differentiates the returned gates,
+    which takes the unfused backward; k = 12 is beyond the fused kernel."""
+    from nanotitan_amd.moe_ops import dispatch_fn, route_count_fn, route_dispatch_fn
+
+    T = 777
+    g = torch.Generator(device="cuda").manual_seed(E + k)
+    X0 = torch.randn(T, d, generator=g, device="cuda").to(dtype)
+    Z0 = torch.randn(T, E, generator=g, device="cuda")
+    dpx = torch.randn(T * k, d, generator=g, device="cuda").to(dtype)
+    dpw = torch.randn(T * k, generator=g, device="cuda")
+    dgt = torch.randn(T, k, generator=g, device="cuda")
+
+    def run(fused):
+        X = X0.clone().requires_grad_(True)
+        Z = Z0.clone().requires_grad_(True)
+        if fused:
+            gates, idx, px, pw, counts, offsets, _tid, inv = route_dispatch_fn(Z, k, X, E)
+        else:
+            gates, idx, ws = route_count_fn(Z, k, X)
+            px, pw, counts, offsets, _tid, inv = dispatch_fn(X, gates, idx, E, ws)
+        loss = (px.float() * dpx.float()).sum() + (pw * dpw).sum()
+        if gates_used:
+            loss = loss + (gates * dgt).sum()
+        loss.backward()
+        return [gates, idx, px, pw, counts, offsets, inv], X.grad, Z.grad
+
+    outs_f, dX_f, dZ_f = run(True)
+    outs_u, dX_u, dZ_u = run(False)
+    torch.cuda.synchronize()
+    for a, b in zip(outs_f, outs_u):
+        assert torch.equal(a.detach(), b.detach())
+    assert torch.equal(dX_f.view(torch.int8), dX_u.view(torch.int8))
+    assert torch.equal(dZ_f.view(torch.int32), dZ_u.view(torch.int32))
