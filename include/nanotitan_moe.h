@@ -206,7 +206,9 @@ int nt_pack_backward_inv(int dtype, const void* dpX, const float* dpw, const int
  * launch when k <= 8: dX as nt_pack_backward_inv, and dlogits [T,E] f32 the
  * router gradient for gates [T,k], topk [T,k] and dgates dw (bit-identical
  * to the two calls). dw [T,k] is optional (NULL: not written) when k <= 8
- * and required above (the two launches then run). Replaces the pack
+ * and required above (the two launches then run). The router's limits hold
+ * (k <= E, k <= 32, E <= NT_MAX_EXPERTS) and are checked before any launch.
+ * Replaces the pack
  * backward (reference csrc/kernels/backward_pack_kernel.cu:10-44) and the
  * backward of the router's softmax / top-k / renormalisation, which the
  * reference leaves to torch autograd (src/model/cuda_backend.py:30-37),

@@ -1054,7 +1054,9 @@ int nt_pack_backward_inv_route(int dtype, const void* dpX, const float* dpw, con
                                int64_t d, int32_t E, void* dX, float* dlogits, float* dw,
                                hipStream_t stream) {
   if (dtype_bytes(dtype) == 0) return NT_ERR_DTYPE;
-  if (!sizes_ok(T, k, d) || k < 1 || E < 1 || E > NT_MAX_EXPERTS) return NT_ERR_INVALID_ARG;
+  // the router's limits (nt_route_topk_backward), checked before any launch
+  if (!sizes_ok(T, k, d) || k < 1 || E < 1 || k > E || k > kMaxTopK) return NT_ERR_INVALID_ARG;
+  if (E > NT_MAX_EXPERTS) return NT_ERR_TOO_MANY_EXPERTS;
   if (T * (int64_t)k > INT32_MAX || T * (int64_t)E > INT32_MAX) return NT_ERR_TOO_LARGE;
   if (T > 0 && (inv == nullptr || dpw == nullptr || gates == nullptr || topk == nullptr ||
                 dlogits == nullptr || (d > 0 && (dpX == nullptr || dX == nullptr))))

@@ -10,6 +10,7 @@
 namespace nt {
 
 constexpr int kWave = 64;
+constexpr int kMaxTopK = 32;  // the router's largest top-k (lane registers per token)
 
 // ---------------------------------------------------------------- elements
 // bf16 and fp16 are carried as raw 16-bit patterns; all arithmetic is fp32.

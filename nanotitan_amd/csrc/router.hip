@@ -24,7 +24,6 @@ namespace {
 
 constexpr int kRouterThreads = 256;
 constexpr int kRouterWaves = kRouterThreads / kWave;
-constexpr int kMaxTopK = 32;
 constexpr int kLanePerExperts = 8;  // target experts per lane
 constexpr int kRouterHistMax = 2048;  // LDS ints of the fused count (see route_topk_hist_kernel)
 

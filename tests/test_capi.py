@@ -102,6 +102,17 @@ def test_workspace_sizes_are_sane():
         ("nt_dispatch_counted", (capi.NT_BF16, None, None, None, 8, 2, 16, 1025, None, None,
                                  None, None, None, None, None, None, 0, None),
          capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_pack_backward_inv_route", (99, None, None, None, None, None, 8, 2, 16, 8, None,
+                                        None, None, None), capi.NT_ERR_DTYPE),
+        ("nt_pack_backward_inv_route", (capi.NT_BF16, None, None, None, None, None, 8, 2, 16,
+                                        1025, None, None, None, None),
+         capi.NT_ERR_TOO_MANY_EXPERTS),
+        ("nt_pack_backward_inv_route", (capi.NT_BF16, None, None, None, None, None, 8, 33, 16,
+                                        64, None, None, None, None), capi.NT_ERR_INVALID_ARG),
+        ("nt_pack_backward_inv_route", (capi.NT_BF16, None, None, None, None, None, 8, 4, 16, 3,
+                                        None, None, None, None), capi.NT_ERR_INVALID_ARG),  # k > E
+        ("nt_pack_backward_inv_route", (capi.NT_BF16, None, None, None, None, None, 8, 2, 16, 8,
+                                        None, None, None, None), capi.NT_ERR_INVALID_ARG),  # nulls
     ],
 )
 def test_argument_errors_return_codes(fn, args, code):
