@@ -2406,9 +2406,12 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
     g.slab_cap = (int32_t)dw_slabs(A, sp);
     g.partial = partial;
   }
+  // 128x128 tiles: three stages, one workgroup per CU (measured on C3's
+  // routing against two stages at two workgroups per CU: 166-170 -> 161-165
+  // us per dW, bit-identical; four stages no better).
   const int st = dw_big_tiles(A, K, N, E, stream)
                      ? launch_mfma<kDw, kEpiPlain, 256, 256, 2, 4, 64, 2>(dtype, g, N, stream)
-                     : launch_mfma<kDw, kEpiPlain, 128, 128, 2, 2, 64, 2>(dtype, g, N, stream);
+                     : launch_mfma<kDw, kEpiPlain, 128, 128, 2, 2, 64, 3>(dtype, g, N, stream);
   if (st != NT_OK || !split) return st;
   return launch_dw_reduce(dtype, offsets, E, A, K, N, sp, partial, dW, stream);
 }
