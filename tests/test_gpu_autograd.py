@@ -296,3 +296,19 @@ def test_route_dispatch_fn_matches_separate_functions(ext, E, k, d, dtype, gates
         assert torch.equal(a.detach(), b.detach())
     assert torch.equal(dX_f.view(torch.int8), dX_u.view(torch.int8))
     assert torch.equal(dZ_f.view(torch.int32), dZ_u.view(torch.int32))
+
+
+def test_route_dispatch_fn_no_tokens(ext):
+    """Zero tokens: empty outputs forward, empty gradients backward (the
+    fused pack + router backward launches nothing)."""
+    from nanotitan_amd.moe_ops import route_dispatch_fn
+
+    X = torch.empty(0, 16, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    Z = torch.empty(0, 8, device="cuda", requires_grad=True)
+    gates, idx, px, pw, counts, offsets, _tid, inv = route_dispatch_fn(Z, 2, X, 8)
+    assert px.shape == (0, 16) and gates.shape == (0, 2) and counts.tolist() == [0] * 8
+    (px.float().sum() + pw.sum()).backward()
+    torch.cuda.synchronize()
+    assert X.grad.shape == (0, 16) and Z.grad.shape == (0, 8)
+    dX, dl = ext.pack_backward_inv_route(px.detach(), pw.detach(), inv, gates.detach(), idx, 8)
+    assert dX.shape == (0, 16) and dl.shape == (0, 8)
