@@ -122,7 +122,11 @@ int32_t nt_dispatch_block_tokens(int64_t T, int32_t k, int64_t d, int dtype);
 
 /* nt_dispatch whose workspace already starts with the per-block counts of
  * nt_route_topk_count (TB = nt_dispatch_block_tokens(T, k, d, dtype)): the
- * same outputs, without the counting pass. */
+ * same outputs, without the counting pass. The counts are only read, so a
+ * second call on the same workspace gives the same outputs; the rest of the
+ * workspace (up to nt_dispatch_workspace_bytes) is scratch the call
+ * overwrites (the counts' scan over blocks, when E times the block count
+ * is above 8192). */
 int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t* topk, int64_t T,
                         int32_t k, int64_t d, int32_t E, int32_t* counts, int32_t* offsets,
                         void* packed_X, int32_t* token_id, int32_t* expert, float* packed_w,
@@ -137,8 +141,9 @@ int nt_dispatch_counted(int dtype, const void* X, const float* w, const int32_t*
  * allocates through torch. The workspace lives in a fixed device array of
  * NT_NOALLOC_SCRATCH_BYTES that the library owns on each GPU it runs on
  * (held until the process ends); sizes whose nt_dispatch_workspace_bytes
- * exceed it return NT_ERR_SCRATCH before any launch (about T/16 * E * 4
- * bytes at 4 KiB rows: 65536 tokens x 128 experts fit). Calls on one GPU
+ * exceed it return NT_ERR_SCRATCH before any launch (two int32 tables of E
+ * x ceil(T/TB) entries plus E bases: 65536 tokens x 128 experts take 2 MiB
+ * at 4 KiB rows). Calls on one GPU
  * share that array and leave its contents behind (nothing in it needs to
  * start at zero); two calls that overlap on one GPU (different streams,
  * not ordered) race on it. Same outputs as nt_dispatch, bit for bit, and no
@@ -257,8 +262,10 @@ int nt_route_topk_backward(const float* gates, const int32_t* topk, const float*
  * bytes when no split can occur. A smaller or NULL
  * workspace is accepted: dW then runs unsplit (and unpaired). Its contents
  * need no initialisation: the counters carry a per-launch tag, and every
- * slab a launch reads it has written. Calls that overlap in time must not
- * share a workspace. */
+ * slab a launch reads it has written. A paired call made while its stream
+ * is being captured into a HIP graph clears its counters with a kernel
+ * launched just before it, so every replay of the graph starts them from
+ * zero. Calls that overlap in time must not share a workspace. */
 size_t nt_grouped_gemm_workspace_bytes(int dtype, int32_t E, int64_t A, int64_t K, int64_t N);
 
 /* out[a,:] = X[a,:] @ W[e] for a in [offsets[e], offsets[e+1]), float32
@@ -335,10 +342,14 @@ int nt_grouped_gemm_dx2(int dtype, const void* W1, const void* W2, const int32_t
 /* dW[e] = X_e^T @ dOut_e summed over the rows of expert e (zero for an empty
  * expert). X [A,K], dOut [A,N], dW [E,K,N]. An expert with more rows than
  * about 1.25 times a workgroup's share of the reduction (skewed routing) is
- * reduced in chunks of about half a share, whose fp32 partials go to ws and
- * are summed in chunk order by a second kernel, so no single tile outlasts
- * the rest. Deterministic: the chunks depend only on the sizes and the
- * device's CU count, fixed summation order, no atomics.
+ * reduced in chunks of about half a share, whose fp32 partials go to ws
+ * and are summed in chunk order, so no single tile outlasts the rest: by a
+ * second kernel here, inside the launch in the paired dW + dX calls (the
+ * last chunk of a tile to arrive sums them). Deterministic: the chunks
+ * depend only on the sizes (the share is planned for 256 CUs on every
+ * device) and every tile is summed in chunk order; the paired calls'
+ * atomic counters only decide which workgroup does the sum, never its
+ * order.
  * Replaces bwd_grouped_gemm_dW_kernel (reference csrc/kernels/bwd_grouped_gemm_dW.cu:43-86). */
 int nt_grouped_gemm_dw(int dtype, const void* X, const int32_t* offsets, const void* dOut,
                        int32_t E, int64_t A, int64_t K, int64_t N, void* dW, void* ws,

@@ -224,7 +224,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_toke
                                                                                    : NT_BF16);
   TORCH_CHECK(ws.is_contiguous() && (size_t)ws.numel() * ws.element_size() >= need,
               "dispatch workspace from route_topk_count is too small for these sizes");
-  // The per-block counts in ws describe these ids; the host pack recounts them.
+  // The per-block counts in ws describe these ids; the host pack recounts
+  // them. ws is left as it is: the counts must survive the call on every
+  // device, and the scratch after them holds nothing the caller reads.
   return dispatch_tokens(X, w, topk, num_experts);
 }
 

@@ -56,16 +56,20 @@ hist_kernel(const int32_t* __restrict__ topk, const int32_t* __restrict__ mask, 
   for (int e = threadIdx.x; e < E; e += blockDim.x) hist[(int64_t)e * nb + b] = s_hist[e];
 }
 
-// Workgroup e: exclusive scan of hist[e, 0..nb) in place, counts[e] = total.
-// With a cursor: base[e] = cursor[e]; cursor[e] += total (the state the
-// reference's atomic cursor is left in, csrc/kernels/pack_tokens.cu:37).
+// Workgroup e: scan[e, 0..nb) = exclusive scan of hist[e, 0..nb),
+// counts[e] = total. `scan` may be `hist` itself (in place); the counted
+// dispatch scans into a region of its own, so the per-block counts the
+// router left in the workspace survive the call. With a cursor: base[e] =
+// cursor[e]; cursor[e] += total (the state the reference's atomic cursor is
+// left in, csrc/kernels/pack_tokens.cu:37).
 __global__ void __launch_bounds__(kDispatchThreads)
-scan_kernel(int32_t* __restrict__ hist, int32_t nb, int32_t* __restrict__ counts,
+scan_kernel(const int32_t* hist, int32_t* scan, int32_t nb, int32_t* __restrict__ counts,
             int32_t* __restrict__ cursor, int32_t* __restrict__ base) {
   __shared__ int32_t s_wsum[kDispatchWaves];
   __shared__ int32_t s_carry;
   const int e = blockIdx.x;
-  int32_t* h = hist + (int64_t)e * nb;
+  const int32_t* h = hist + (int64_t)e * nb;
+  int32_t* o = scan + (int64_t)e * nb;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   if (threadIdx.x == 0) s_carry = 0;
@@ -78,7 +82,7 @@ scan_kernel(int32_t* __restrict__ hist, int32_t nb, int32_t* __restrict__ counts
     __syncthreads();
     int before = s_carry;
     for (int w = 0; w < wave; ++w) before += s_wsum[w];
-    if (i < nb) h[i] = before + incl - v;
+    if (i < nb) o[i] = before + incl - v;
     __syncthreads();
     if (threadIdx.x == 0) {
       int tot = 0;
@@ -354,8 +358,15 @@ size_t hist_bytes(const PackPlan& p, int32_t E) {
   return (size_t)round_up((int64_t)E * p.nb * 4, 256);
 }
 
+// [hist | base | scan]: the per-block histogram, the per-expert bases of
+// nt_pack_tokens, and the counted dispatch's scan of the histogram (kept
+// apart from it, so that the histogram is only read).
 size_t dispatch_ws_bytes(const PackPlan& p, int32_t E) {
-  return hist_bytes(p, E) + (size_t)round_up((int64_t)E * 4, 256);
+  return 2 * hist_bytes(p, E) + (size_t)round_up((int64_t)E * 4, 256);
+}
+int32_t* scan_region(void* ws, const PackPlan& p, int32_t E) {
+  return reinterpret_cast<int32_t*>(static_cast<char*>(ws) + hist_bytes(p, E) +
+                                    (size_t)round_up((int64_t)E * 4, 256));
 }
 
 int nbits_for(int32_t E) {
@@ -424,8 +435,8 @@ int launch_hist_scan(const PackPlan& plan, const int32_t* topk, const int32_t* m
     int st = launch_status();
     if (st != NT_OK) return st;
   }
-  hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, plan.nb,
-                     counts, cursor, base);
+  hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, hist,
+                     plan.nb, counts, cursor, base);
   return launch_status();
 }
 
@@ -517,9 +528,13 @@ int dispatch_impl(int dtype, const void* X, const float* w, const int32_t* topk,
       st = launch_status();
     }
   } else if (counted) {
-    hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, plan.nb,
-                       counts, nullptr, nullptr);
+    // The router's counts stay as they are: a second call on the same
+    // workspace sees the same histogram.
+    int32_t* scan = scan_region(ws, plan, E);
+    hipLaunchKernelGGL(scan_kernel, dim3(E), dim3(kDispatchThreads), 0, stream, hist, scan,
+                       plan.nb, counts, nullptr, nullptr);
     st = launch_status();
+    hist = scan;
   } else {
     st = launch_hist_scan(plan, topk, nullptr, T, k, E, hist, counts, nullptr, nullptr, stream);
   }

@@ -469,6 +469,66 @@ __device__ __forceinline__ void tile_coords(int64_t logical, int64_t mtiles, int
   nt = (int)(rem / gsz);
 }
 
+// Row-tiled modes (forward, dX): logical tile -> (expert, m-tile within the
+// expert, n-tile). Expert e's tiles are the block [P_e * ntn, P_{e+1} * ntn)
+// of the logical order (P = s_pref, its m-tile prefix), so that tiles
+// which run at the same time share the expert's weight panels. Inside the
+// block the expert's m-tiles form ceil(mt_e / kGroupM) groups of balanced
+// sizes (never crossing into the next expert, and with no stub group for
+// an expert one m-tile past a multiple of kGroupM), each walked m fastest.
+__device__ __forceinline__ void expert_tile_coords(int64_t logical, const int32_t* s_pref, int E,
+                                                   int ntn, int& e_out, int64_t& mtl, int& nt) {
+  const int64_t mt_global = logical / ntn;
+  int lo = 0, hi = E - 1;  // largest e with s_pref[e] <= mt_global
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt_global) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t mt_e = s_pref[lo + 1] - s_pref[lo];
+  const int64_t l = logical - (int64_t)s_pref[lo] * ntn;
+  const int64_t ng = ceil_div(mt_e, (int64_t)kGroupM);
+  const int64_t base = mt_e / ng, rem = mt_e % ng;  // rem groups of base + 1, then base
+  const int64_t big = rem * (base + 1) * ntn;       // tiles in the larger groups
+  int64_t gi, gsz, gm0;
+  if (l < big) {
+    gi = l / ((base + 1) * ntn);
+    gsz = base + 1;
+    gm0 = gi * (base + 1);
+  } else {
+    gi = (l - big) / (base * ntn);
+    gsz = base;
+    gm0 = rem * (base + 1) + gi * base;
+    gi += rem;
+  }
+  const int64_t r = l - gm0 * ntn;
+  e_out = lo;
+  mtl = gm0 + r % gsz;
+  nt = (int)(r / gsz);
+}
+
+// Start of the logical-tile range of the workgroups before `before` (of G):
+// the proportional share, moved to the nearest expert boundary when that
+// is within 1/16 of one XCD's share (so an XCD's range holds whole experts
+// where the routing allows it, without unbalancing the XCDs).
+__device__ __forceinline__ int64_t xcd_range_start(int64_t total, int64_t before, int64_t G,
+                                                   const int32_t* s_pref, int E, int ntn) {
+  const int64_t b = total * before / G;
+  if (b <= 0 || b >= total) return b;
+  const int64_t mt = b / ntn;
+  int lo = 0, hi = E - 1;  // largest e with s_pref[e] <= mt
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t e0 = (int64_t)s_pref[lo] * ntn, e1 = (int64_t)s_pref[lo + 1] * ntn;
+  const int64_t near = (b - e0 <= e1 - b) ? e0 : e1;
+  const int64_t tol = total / 8 / 16;
+  const int64_t dist = near > b ? near - b : b - near;
+  return dist <= tol ? near : b;
+}
+
 // Operand pointers, strides and valid extents of one output tile, for
 // elements of storage type U (uint16_t: bf16 / fp16; float).
 template <typename U>
@@ -513,9 +573,9 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
   j.pf0 = nullptr;
   j.nch = 1;
   j.done_idx = 0;
-  int64_t mt;
-  int nt;
-  tile_coords(logical, mtiles, g.ntn, mt, nt);
+  int64_t mt = 0;
+  int nt = 0;
+  if (MODE == kDw) tile_coords(logical, mtiles, g.ntn, mt, nt);
   if (MODE == kDw) {
     // m-tile = (reduction chunk, K tile); s_pref / s_split: build_chunk_prefix.
     const int32_t* s_split = s_pref + (NT_MAX_EXPERTS + 1);
@@ -555,8 +615,10 @@ __device__ __forceinline__ void setup_job(const GemmArgs& g, const int32_t* s_pr
   } else {
     int e;
     int64_t r0, r1, mtl;
-    find_m_tile(g.offsets, g.E, g.A, s_pref, mt, e, r0, r1, mtl);
+    expert_tile_coords(logical, s_pref, g.E, g.ntn, e, mtl, nt);
+    expert_rows(g.offsets, e, g.A, r0, r1);
     e = __builtin_amdgcn_readfirstlane(e);
+    nt = __builtin_amdgcn_readfirstlane(nt);
     r0 = (int64_t)__builtin_amdgcn_readfirstlane((int)r0);
     r1 = (int64_t)__builtin_amdgcn_readfirstlane((int)r1);
     mtl = (int64_t)__builtin_amdgcn_readfirstlane((int)mtl);
@@ -1251,8 +1313,12 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   const int64_t q = G / kXcd, r = G % kXcd;
   const int64_t before = xcd * q + (xcd < r ? xcd : r);
   const int64_t nbx = q + (xcd < r ? 1 : 0);  // workgroups on this XCD
-  const int64_t t_end = total * (before + nbx) / G;
-  int64_t logical = total * before / G + wg / kXcd;
+  // Row-tiled modes snap the XCD ranges to expert boundaries where they can.
+  const int64_t t_end = MODE == kDw ? total * (before + nbx) / G
+                                    : xcd_range_start(total, before + nbx, G, s_pref, g.E, g.ntn);
+  int64_t logical = (MODE == kDw ? total * before / G
+                                 : xcd_range_start(total, before, G, s_pref, g.E, g.ntn)) +
+                    wg / kXcd;
   // Dynamic order (DYN): the tiles form kXcd contiguous parts;
   // workgroup wg takes the next tile of its XCD's part from the epoch-tagged
   // counter dyn[p] (claim_tagged), then those of the following parts. One
@@ -2427,6 +2493,13 @@ int dw_impl(int dtype, const void* X, const int32_t* offsets, const void* dOut, 
 // to the two separate calls (every output tile is reduced in the same
 // order).
 constexpr int32_t kPairMaxExperts = 16;
+constexpr int kXcdParts = 8;  // claim counters of a paired launch (one per XCD part)
+
+__global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
 
 // Epochs of the paired launches' claim counters: 40 bits, a different
 // value per launch in this process, starting from a value drawn from the
@@ -2488,6 +2561,23 @@ int pair_dw_dx(int dtype, const void* X, const int32_t* offsets, const void* dOu
     // the split tiles sum their slabs in the launch (no reduce pass)
     gw.done = reinterpret_cast<unsigned long long*>(partial + dw_slabs(A, sp) * K * N);
     gw.done_epoch = epoch;
+  }
+  // Under stream capture the graph replays this launch with the epoch it
+  // was captured with, so the counters would still hold the previous
+  // replay's final counts under that same epoch (every dX claim would fail,
+  // no split tile would be the last to arrive). A captured call clears them
+  // first, with a fill kernel that is part of the graph (a memset node is
+  // avoided: such nodes have given wrong results on replays here).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusActive) {
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(1), dim3(256), 0, stream, dyn, (int64_t)kXcdParts);
+    if (split) {
+      const int64_t ndone = (int64_t)dw_slabs(A, sp) * ceil_div(K, 256) * ceil_div(N, 256);
+      hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(ndone, 256), 1024)),
+                         dim3(256), 0, stream, gw.done, ndone);
+    }
+    const int st = launch_status();
+    if (st != NT_OK) return st;
   }
   plan_tiles<kDw>(gw, N, 256, 256);
   plan_tiles<kDx>(gx, K, 256, 256);

@@ -636,7 +636,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_toke
 }
 
 // dispatch_tokens starting from the per-block counts route_topk_count left
-// in `ws` (no counting pass).
+// in `ws` (no counting pass). The counts stay as they are (a second call on
+// the same ws gives the same outputs); the rest of ws is overwritten scratch.
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> dispatch_tokens_counted(
     Tensor X, Tensor w, Tensor topk, int64_t num_experts, Tensor ws) {
   return dispatch_impl(X, w, topk, num_experts, ws);
@@ -962,8 +963,11 @@ TORCH_LIBRARY(nanotitan, m) {
   m.def("route_topk_backward(Tensor gates, Tensor topk, Tensor dgates, int num_experts) -> Tensor");
   m.def("dispatch_tokens(Tensor X, Tensor topk_weights, Tensor topk_experts, int num_experts) "
         "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  // ws: the per-block counts at its start are only read; the rest is scratch
+  // the HIP kernel overwrites (so the schema marks it mutable).
   m.def("dispatch_tokens_counted(Tensor X, Tensor topk_weights, Tensor topk_experts, "
-        "int num_experts, Tensor ws) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+        "int num_experts, Tensor(a!) ws) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, "
+        "Tensor)");
   m.def("pack_tokens_inv(Tensor X, Tensor topk_weights, Tensor topk_experts, "
         "Tensor(a!) expert_offset_cpy) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("combine_inv(Tensor expert_outputs, Tensor inv, Tensor packed_topk_weights, "

@@ -237,3 +237,47 @@ def test_route_count_rejects_small_workspace(ext):
         ext.dispatch_tokens_counted(X, g, i, 8, ws[:4])
     with pytest.raises(RuntimeError):
         ext.route_topk_count(logits, 2, X[:10])
+
+
+@pytest.mark.parametrize("cfg_id,T,d", [(3, 30720, 512), (5, 65536, 2048), (2, 30720, 512)])
+def test_counted_dispatch_keeps_the_counts(ext, cfg_id, T, d):
+    """dispatch_tokens_counted only reads the per-block counts at the start
+    of its workspace: they are unchanged after a call, and a second call on
+    the same workspace gives the same bits. C3 and C5 routing take the
+    separate scan launch (E x blocks above the in-pack fold limit), which
+    writes the workspace's scratch after the counts; C2 the fold."""
+    from nanotitan_amd import capi
+
+    dd = O.make_inputs(cfg_id, T=T, with_weights=False)
+    c = dd["cfg"]
+    X = dd["X"][:, :d].contiguous().cuda()
+    g, i, ws = ext.route_topk_count(dd["logits"].cuda(), c.k, X)
+    TB = capi.load().nt_dispatch_block_tokens(T, c.k, d, capi.dtype_code(X.dtype))
+    nb = -(-T // TB)
+    counts_bytes = c.E * nb * 4
+    before = ws[:counts_bytes].clone()
+    first = ext.dispatch_tokens_counted(X, g, i, c.E, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(ws[:counts_bytes], before)
+    second = ext.dispatch_tokens_counted(X, g, i, c.E, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(ws[:counts_bytes], before)
+    for a, b in zip(first, second):
+        assert torch.equal(bits(a), bits(b))
+    want = np.bincount(O.route(dd["logits"], c.k)[1].numpy().ravel(), minlength=c.E)
+    assert np.array_equal(first[0].cpu().numpy(), want)
+    assert (c.E * nb > 8192) == (cfg_id in (3, 5))  # the separate scan path at C3 / C5
+
+
+def test_counted_dispatch_opcheck_on_gpu(ext):
+    """torch.library.opcheck on device tensors: the schema (workspace
+    marked mutable) and the fake kernel agree with what the HIP op does."""
+    from nanotitan_amd.extension import load_op_library
+
+    load_op_library()
+    dd = O.make_inputs(3, T=16384, with_weights=False)  # 64 experts x 256 blocks: the scan launch
+    c = dd["cfg"]
+    X = dd["X"][:, :64].contiguous().cuda()
+    g, i, ws = torch.ops.nanotitan.route_topk_count(dd["logits"].cuda(), c.k, X)
+    torch.library.opcheck(torch.ops.nanotitan.dispatch_tokens_counted.default,
+                          (X, g, i, c.E, ws), test_utils=("test_schema", "test_faketensor"))

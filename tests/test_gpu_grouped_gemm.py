@@ -418,3 +418,51 @@ def test_f32_mfma_tails_and_empty_experts(ext, K, N, counts):
     for e, c in enumerate(counts):
         if c == 0:
             assert not dW[e].any()
+
+
+@pytest.mark.parametrize("counts,K,N", [([7680] * 8, 2048, 512), ([20000, 0, 3, 9000, 5000], 1024, 256)])
+def test_paired_dw_dx_under_graph_replay(ext, counts, K, N):
+    """A paired dW + dX call captured into a HIP graph: every replay equals
+    the eager call on the inputs of that replay, bit for bit. The graph
+    replays the launch with the tag it was captured with, so the call clears
+    its claim (and, for the split head expert of the second case, arrival)
+    counters with a kernel captured just before it; without that, the
+    second replay would find the first one's final counts. Eager work and
+    synchronisations run between the replays."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(K + len(counts))
+    A, E = sum(counts), len(counts)
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    og = offsets.cuda()
+    X = torch.empty(A, K, dtype=dtype, device="cuda")
+    W = torch.empty(E, K, N, dtype=dtype, device="cuda")
+    dOut = torch.empty(A, N, dtype=dtype, device="cuda")
+
+    def fill(seed):
+        gg = torch.Generator().manual_seed(seed)
+        X.copy_(torch.randn(A, K, generator=gg).to(dtype))
+        W.copy_((torch.randn(E, K, N, generator=gg) / K ** 0.5).to(dtype))
+        dOut.copy_(torch.randn(A, N, generator=gg).to(dtype))
+
+    fill(0)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the allocator outside the capture
+        ext.bwd_grouped_gemm_dW_dX(X, W, og, dOut)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dW_g, dX_g = ext.bwd_grouped_gemm_dW_dX(X, W, og, dOut)
+    for seed in (1, 2, 3, 4):
+        fill(seed)
+        dW_e = ext.bwd_grouped_gemm_dW_kernel(X, og, dOut)  # eager, separate calls
+        dX_e = ext.bwd_grouped_gemm_dX_kernel(W, og, dOut)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[graph] replay with inputs of seed {seed}", flush=True)
+        assert torch.equal(dW_g.view(torch.int16), dW_e.view(torch.int16)), seed
+        assert torch.equal(dX_g.view(torch.int16), dX_e.view(torch.int16)), seed

@@ -355,6 +355,20 @@ def test_opcheck(ops, name):
                           test_utils=("test_schema", "test_faketensor"))
 
 
+def test_opcheck_counted_dispatch(ops):
+    """The counted dispatch's schema marks its workspace mutable (the HIP
+    kernel writes scratch after the router's counts); opcheck's schema and
+    fake-tensor checks agree with the CPU kernel."""
+    a = _cases()
+    X, w, topk, E = a["dispatch_tokens"]
+    logits, k = a["route_topk"]
+    g, i, ws = ops.route_topk_count(logits, k, X)
+    torch.library.opcheck(torch.ops.nanotitan.dispatch_tokens_counted.default, (X, g, i, E, ws),
+                          test_utils=("test_schema", "test_faketensor"))
+    sch = torch.ops.nanotitan.dispatch_tokens_counted.default._schema
+    assert sch.arguments[4].alias_info is not None and sch.arguments[4].alias_info.is_write
+
+
 def test_cpu_ops_check_arguments_like_the_gpu_ops(ops):
     """Same TORCH_CHECK conditions (and messages) as the HIP surface."""
     T, k, d = 16, 2, 8

@@ -55,9 +55,13 @@ def _bits(t):
 def test_noalloc_dispatch_matches_dispatch_twice(lib, dtype):
     s = current_stream()
     dc = dtype_code(dtype)
-    # The second call is smaller (fewer tokens, experts and columns): it must
-    # not depend on what the first one left in the scratch.
-    for T, k, E, d, seed in [(30720, 2, 8, 512, 1), (3001, 8, 64, 256, 2)]:
+    # Each call after the first is smaller than one before it (fewer tokens,
+    # experts or columns): it must not depend on what those left in the
+    # scratch. 128 experts over 1024 and 313 token blocks take the separate
+    # histogram scan (above 8192 entries); the others sum the histogram
+    # inside the pack.
+    for T, k, E, d, seed in [(65536, 8, 128, 256, 3), (30720, 2, 8, 512, 1),
+                             (20000, 8, 128, 128, 4), (3001, 8, 64, 256, 2)]:
         X, w, topk = _inputs(T, k, E, d, dtype, seed)
         print(f"[no-alloc] T={T} k={k} E={E} d={d} {dtype}", flush=True)
         ref = _outputs(T, k, E, d, dtype)
