@@ -12,8 +12,12 @@ data, random-init weights.
 Prints ONE JSON line:
 
 * ``value``: tokens/s over K timed steps with only the step's own launches
-  on the stream, after W warmup steps launched the same way (the GPU's clocks
-  settle over the first ~20 back-to-back steps; the default W is past that).
+  on the stream, after W warmup steps launched the same way. The headline
+  runs after the other GPU legs below (which do not touch its timing). In a
+  fresh process the first 20-30 back-to-back C2 steps run 10-25% slower than
+  later ones (measured step by step on MI355X; running the other legs
+  first does not remove this), so a short W reads a few percent slower
+  than the steady state.
 * ``roofline``: the dominant kernel family (the grouped GEMMs): algorithmic
   FLOPs per launch (2*A*K*N) over the average launch duration, measured with
   HIP events on the launch stream around every launch in a second timed pass
@@ -26,16 +30,20 @@ Prints ONE JSON line:
   the repetitions.
   ``copy_ceiling``: the library's own 16-byte streaming copy under the same
   cold rule, at about the HBM kernels' sizes, the achievable bandwidth they
-  are measured against.
+  are measured against, and beside it a write-only fill and a read-only pass
+  of the same byte counts (the ceilings of write- and read-dominated mixes).
 * ``configs``: the other BASELINE.json configs (C1, C3, C4, C5) through the
   same measurement with fewer steps: ms/step, tokens/s, GEMM TF/s and its
   fraction of the roof, the HBM kernels in the layer and cold.
 * ``cpu_baseline``: the CPU restatement of the reference torch path on the
-  first tokens of the headline inputs (rank 0, N=1 only).
+  headline inputs, all of them when 1 warmup + 3 timed iterations fit the
+  budget (C2 does), else their first tokens (rank 0, N=1 only); and
+  ``configs.C1.cpu_baseline``: the same on C1 (fp32, the reference CPU
+  path's config), 2 warmup + 5 timed iterations.
 
-Headline inputs are drawn on the CPU with a seeded generator and copied to
-the GPU, so the CPU baseline runs on the same bits; the secondary configs are
-drawn on the GPU (no CPU run uses them).
+Headline and C1 inputs are drawn on the CPU with a seeded generator and
+copied to the GPU, so the CPU baselines run on the same bits; the other
+configs are drawn on the GPU (no CPU run uses them).
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--config 2]
        [--ffn gelu|swiglu] [--configs all|none|1,3,...]
@@ -367,12 +375,26 @@ def family_report(fams, wl):
     return kernels
 
 
+_SINK = {}
+
+
+def _flush(scratch):
+    """Read all of `scratch` with the library's streaming read (evicts the
+    L2s and the Infinity Cache; no temporaries, nothing written)."""
+    from nanotitan_amd.extension import get_hip_extension
+
+    dev = scratch.device
+    if dev not in _SINK:
+        _SINK[dev] = torch.zeros(1, dtype=torch.int32, device=dev)
+    get_hip_extension().stream_read(scratch, _SINK[dev])
+
+
 def _cold_median(fn, scratch, reps):
     """Median device time of fn() (HIP events on the current stream), each
     launch preceded by a full read of `scratch` outside the events."""
     times = []
     for _ in range(reps):
-        scratch.sum(dtype=torch.int64)
+        _flush(scratch)
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
@@ -416,7 +438,10 @@ def copy_ceiling(ext, scratch, reps=10):
     """The library's streaming copy (nt_stream_copy), cold, at about the
     bytes the HBM kernels move (C2: 95 and 158 MB, C4: 400 MB, C5: 2.4 GB):
     GB/s of bytes read + written. Short copies do not reach the long ones'
-    rate (launch fill and drain), so each kernel compares with its size."""
+    rate (launch fill and drain), so each kernel compares with its size.
+    Beside it, at the same byte counts, the write-only fill (nt_stream_fill:
+    the ceiling of a kernel that mostly writes, like the dispatch's k copies
+    of each row) and the read-only pass (nt_stream_read)."""
     out = {}
     for label, moved in (("moved_95MB", 95e6), ("moved_158MB", 158e6), ("moved_400MB", 400e6),
                          ("moved_2400MB", 2400e6)):
@@ -429,6 +454,16 @@ def copy_ceiling(ext, scratch, reps=10):
         out[label] = {"us": round(ms * 1e3, 1), "GB_s": round(gbs, 1),
                       "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
         del src, dst
+        buf = torch.empty(2 * n, dtype=torch.uint8, device="cuda")
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        for kind, fn in (("write", lambda: ext.stream_fill(buf, 0)),
+                         ("read", lambda: ext.stream_read(buf, sink))):
+            fn()
+            ms = _cold_median(fn, scratch, reps)
+            gbs = 2.0 * n / (ms * 1e-3) / 1e9
+            out[label.replace("moved", kind)] = {"us": round(ms * 1e3, 1), "GB_s": round(gbs, 1),
+                                                 "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+        del buf
     torch.cuda.empty_cache()
     return out
 
@@ -444,9 +479,11 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(wl_cpu, budget_s: float = 20.0):
-    """The reference torch CPU path (oracle restatement) on the first tokens of
-    the same inputs the GPU ran (drawn on the CPU), sized to ~budget_s."""
+def cpu_baseline(wl_cpu, budget_s: float = 20.0, warmup: int = 1, max_iters: int = 3):
+    """The reference torch CPU path (oracle restatement) on the same inputs
+    the GPU ran (drawn on the CPU): the whole workload when `warmup` +
+    `max_iters` iterations fit in about budget_s (C2: 1 + 3, C1: 2 + 5, as
+    planned for the baseline), else its first tokens, sized to ~budget_s."""
     from oracle import moe_oracle as O
 
     host_cores = os.cpu_count() or 1
@@ -466,13 +503,15 @@ def cpu_baseline(wl_cpu, budget_s: float = 20.0):
     t0 = time.perf_counter()
     layer(T)
     per_token = (time.perf_counter() - t0) / T
-    T = int(min(T0, 4096, max(256, budget_s / 4 / per_token)) // 256 * 256)
-    print(f"bench.py: cpu_baseline sample {T} tokens (~{per_token * T:.1f} s per iteration)",
-          file=sys.stderr, flush=True)
+    fit = budget_s / (warmup + max_iters) / per_token
+    T = T0 if fit >= T0 else int(max(256, fit) // 256 * 256)
+    print(f"bench.py: cpu_baseline {wl_cpu['name']} sample {T} tokens "
+          f"(~{per_token * T:.2f} s per iteration)", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
-    layer(T)  # warmup
-    first = time.perf_counter() - t0
-    iters = max(1, min(3, int(budget_s / max(first, 1e-3))))
+    for _ in range(warmup):
+        layer(T)
+    first = (time.perf_counter() - t0) / max(warmup, 1)
+    iters = max(1, min(max_iters, int(budget_s / max(first, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(iters):
         layer(T)
@@ -484,9 +523,12 @@ def cpu_baseline(wl_cpu, budget_s: float = 20.0):
         "host_cores": host_cores,
         "thread_cap": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
-        "sample": f"{wl_cpu['name']} headline inputs (seed {wl_cpu['seed']}, drawn on the CPU, "
-                  f"the same bits the GPU ran): first {T} of {T0} tokens, {wl_cpu['dtype']}, "
-                  f"1 warmup + {iters} timed fwd+bwd iterations on {torch.get_num_threads()} "
+        "tokens": T,
+        "sample": f"{wl_cpu['name']} inputs (seed {wl_cpu['seed']}, drawn on the CPU, "
+                  f"the same bits the GPU ran): "
+                  + (f"all {T0} tokens" if T == T0 else f"first {T} of {T0} tokens")
+                  + f", {wl_cpu['dtype']}, "
+                  f"{warmup} warmup + {iters} timed fwd+bwd iterations on {torch.get_num_threads()} "
                   f"threads of {host_cores} host cores (thread cap OMP_NUM_THREADS="
                   f"{os.environ.get('OMP_NUM_THREADS', 'unset')}); host CPU: {cpu_model()}; "
                   f"torch {torch.__version__}",
@@ -596,6 +638,50 @@ def main():
 
     torch.manual_seed(0)
     wl_cpu = make_workload(args.config, "cpu", draw="cpu")
+
+    # The other GPU legs (cold-cache kernel timings, copy ceilings, the other
+    # configs) run first and the headline last.
+    scratch = torch.ones(SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
+    wl = {k: (v.to("cuda") if isinstance(v, torch.Tensor) else v) for k, v in wl_cpu.items()}
+    kernels_cold = cold_hbm_kernels(ext, wl, scratch, args.cold_reps)
+    ceiling = copy_ceiling(ext, scratch, args.cold_reps)
+    del wl
+    torch.cuda.empty_cache()
+
+    configs = {}
+    cpu_configs = {}
+    if args.configs != "none":
+        ids = sorted(WORKLOADS) if args.configs == "all" else [int(c) for c in args.configs.split(",")]
+        for cid in ids:
+            if cid == args.config:
+                continue
+            # C1 (the CPU path's own config, 4096 tokens) is drawn on the CPU,
+            # so its CPU baseline runs on the bits the GPU ran.
+            if cid == 1:
+                w_cpu = make_workload(cid, "cpu", draw="cpu")
+                w2 = {k: (v.to("cuda") if isinstance(v, torch.Tensor) else v)
+                      for k, v in w_cpu.items()}
+                cpu_configs[w2["name"]] = w_cpu
+            else:
+                w2 = make_workload(cid, "cuda", draw="device")
+            e2, ee2, f2 = run_layer(timer, w2, args.config_steps, args.config_warmup, args.ffn)
+            rep = family_report(f2, w2)
+            configs[w2["name"]] = {
+                "workload": f"{w2['T']} tokens x d={w2['d']}, E={w2['E']}, top-{w2['k']}, "
+                            f"FFN {w2['d']}->{w2['f']}->{w2['d']}, {w2['dtype']}",
+                "tokens_per_s": round(w2["T"] * args.config_steps / e2, 1),
+                "ms_per_step": round(e2 / args.config_steps * 1e3, 4),
+                "steps": args.config_steps,
+                "warmup": args.config_warmup,
+                "gemm": rep.pop("gemm", None),
+                "hbm_in_layer": rep,
+                "hbm_cold": cold_hbm_kernels(ext, w2, scratch, args.cold_reps),
+            }
+            del w2
+            torch.cuda.empty_cache()
+    del scratch
+    torch.cuda.empty_cache()
+
     wl = {k: (v.to("cuda") if isinstance(v, torch.Tensor) else v) for k, v in wl_cpu.items()}
     elapsed, elapsed_events, fams = run_layer(timer, wl, args.steps, args.warmup, args.ffn)
 
@@ -620,36 +706,7 @@ def main():
     }
     roofline.update(profile_fields(wl, args.ffn))
     kernels = family_report(fams, wl)
-
-    scratch = torch.ones(SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
-    kernels_cold = cold_hbm_kernels(ext, wl, scratch, args.cold_reps)
-    ceiling = copy_ceiling(ext, scratch, args.cold_reps)
     del wl
-    torch.cuda.empty_cache()
-
-    configs = {}
-    if args.configs != "none":
-        ids = sorted(WORKLOADS) if args.configs == "all" else [int(c) for c in args.configs.split(",")]
-        for cid in ids:
-            if cid == args.config:
-                continue
-            w2 = make_workload(cid, "cuda", draw="device")
-            e2, ee2, f2 = run_layer(timer, w2, args.config_steps, args.config_warmup, args.ffn)
-            rep = family_report(f2, w2)
-            configs[w2["name"]] = {
-                "workload": f"{w2['T']} tokens x d={w2['d']}, E={w2['E']}, top-{w2['k']}, "
-                            f"FFN {w2['d']}->{w2['f']}->{w2['d']}, {w2['dtype']}",
-                "tokens_per_s": round(w2["T"] * args.config_steps / e2, 1),
-                "ms_per_step": round(e2 / args.config_steps * 1e3, 4),
-                "steps": args.config_steps,
-                "warmup": args.config_warmup,
-                "gemm": rep.pop("gemm", None),
-                "hbm_in_layer": rep,
-                "hbm_cold": cold_hbm_kernels(ext, w2, scratch, args.cold_reps),
-            }
-            del w2
-            torch.cuda.empty_cache()
-    del scratch
     torch.cuda.empty_cache()
 
     name, dtype_, T, d, E, k, f, _ws, _ls = WORKLOADS[args.config]
@@ -687,6 +744,9 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl_cpu, args.cpu_budget)
+        for name, w_cpu in cpu_configs.items():  # C1: 2 warmup + 5 timed iterations
+            configs[name]["cpu_baseline"] = cpu_baseline(w_cpu, args.cpu_budget, warmup=2,
+                                                         max_iters=5)
     print(json.dumps(result), flush=True)
 
 

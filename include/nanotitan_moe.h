@@ -76,6 +76,15 @@ int nt_version(void);
  * (csrc/kernels/copy_kernel.cu:25-36, benchmarks/mem_copy_benchmark.py:52-95). */
 int nt_stream_copy(void* dst, const void* src, size_t bytes, int32_t blocks, hipStream_t stream);
 
+/* Write-only and read-only ceilings beside the copy: dst[0..bytes) = value
+ * (as 32-bit words), and a read of src[0..bytes) that writes nothing
+ * (`sink`, one word, is written only if the XOR of the data happens to equal
+ * a fixed constant). bytes and the pointers 16-byte aligned. Measurement
+ * references for kernels whose traffic is mostly writes or mostly reads; no
+ * counterpart in the reference. */
+int nt_stream_fill(void* dst, size_t bytes, uint32_t value, hipStream_t stream);
+int nt_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
+
 /* ------------------------------------------------------------------ dispatch */
 
 /* Workspace for nt_count_experts / nt_pack_tokens / nt_dispatch with these

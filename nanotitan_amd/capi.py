@@ -9,7 +9,7 @@ signature; ``load()`` checks that the library exports all of them.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_char_p, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import c_char_p, c_int, c_int32, c_int64, c_size_t, c_uint32, c_void_p
 from functools import lru_cache
 
 from nanotitan_amd.extension import LIB_PATH
@@ -32,6 +32,8 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
     "nt_strerror": (c_char_p, [c_int]),
     "nt_version": (c_int, []),
     "nt_stream_copy": (c_int, [_P, _P, c_size_t, c_int32, _P]),
+    "nt_stream_fill": (c_int, [_P, c_size_t, c_uint32, _P]),
+    "nt_stream_read": (c_int, [_P, c_size_t, _P, _P]),
     "nt_dispatch_workspace_bytes": (c_size_t, [c_int64, c_int32, c_int32, c_int64, c_int]),
     "nt_count_experts": (
         c_int,

@@ -1053,27 +1053,36 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
   }
 }
 
-// Epilogue of the 8-wave kernel with split duties (plain and two-part
-// epilogues): waves NW/2..NW-1 issue every global store of the tile and
-// never wait for them, so the stores drain behind the next tile's k-loop
-// (vmcnt is per wave and retires in issue order: a wave that also issued the
-// operand loads would wait for its stores at its next load wait). Each round
-// every wave rounds a 16-row half of one of its 32-row sub-tiles into its LDS
-// scratch region; after a barrier storer wave w reads back its own region
-// and that of wave w - NW/2 (16 bytes per lane, whole 128-byte row segments)
-// and stores both; a second barrier frees the scratch for the next round.
-// `scratch` holds split_scratch_bytes<TN>(NW) bytes.
-template <int TN>
+// Epilogue of the 8-wave kernel with split duties (plain, two-part and
+// GELU epilogues): waves NW/2..NW-1 issue every global store of the tile
+// and never wait for them, so the stores drain behind the next tile's
+// k-loop (vmcnt is per wave and retires in issue order: a wave that also
+// issued the operand loads would wait for its stores at its next load
+// wait). Each round every wave rounds a 16-row half of one of its 32-row
+// sub-tiles into its LDS scratch region (for the GELU epilogue it also
+// computes gelu and gelu' of the rounded values there, so that VALU work is
+// shared by all the waves, and writes both into two regions); after a
+// barrier storer wave w reads back its own region(s) and those of wave
+// w - NW/2 (16 bytes per lane, whole 128-byte row segments) and stores
+// them; a second barrier frees the scratch for the next round.
+// `scratch` holds split_scratch_bytes<TN, EPI>(NW) bytes.
+template <int TN, int EPI = kEpiPlain>
 constexpr int split_scratch_bytes(int nw) {
-  return nw * 16 * epi_pitch<TN>();
+  return (EPI == kEpiGelu ? 2 : 1) * nw * 16 * epi_pitch<TN>();
 }
-template <typename T, int TM, int TN, int WGN, int WM, int WN, int NW>
+template <typename T, int TM, int TN, int WGN, int WM, int WN, int NW, int EPI = kEpiPlain,
+          bool TAB = false>
 __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], const TileJob& j,
-                                                 int wave, int lane, char* scratch) {
+                                                 int wave, int lane, char* scratch,
+                                                 const uint32_t* tab = nullptr) {
   static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
+  static_assert(EPI == kEpiPlain || EPI == kEpiDualK || EPI == kEpiGelu,
+                "plain, two-part or GELU epilogue");
+  constexpr bool kGelu = EPI == kEpiGelu;
   constexpr int ROWS = 16;
   constexpr int kPitch = epi_pitch<TN>();
   constexpr int kRegion = ROWS * kPitch;  // one wave's half sub-tile
+  constexpr int kOut2 = NW * kRegion;     // GELU: gelu' regions follow the gelu ones
   constexpr int kLanesPerRow = TN * 4;
   constexpr int kRowsPerRead = 64 / kLanesPerRow;
   constexpr int kQ = ROWS / kRowsPerRead;
@@ -1085,6 +1094,7 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
   const uint32_t ldo = (uint32_t)j.ldo;
   char* mine = scratch + wave * kRegion;
   const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
+  const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(kGelu ? j.po2 : j.po);
   const int r = lane & 31;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -1092,15 +1102,42 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
     for (int ps = 0; ps < 32 / ROWS; ++ps) {
       if (r / ROWS == ps) {
         char* row = mine + (r % ROWS) * kPitch;
+        uint32_t w[2 * TN * 4];
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
-            const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
-            *reinterpret_cast<uint2*>(row + c * 2) =
-                make_uint2(pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]),
-                           pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]));
+            w[2 * (4 * jn + gq)] = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
+            w[2 * (4 * jn + gq) + 1] = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
           }
+        if constexpr (kGelu) {
+          // gelu and gelu' of the rounded h (h itself is not stored)
+          uint32_t g1[2 * TN * 4], g2[2 * TN * 4];
+          if constexpr (TAB) {
+            gelu_table<2 * TN * 4>(w, tab, g1, g2);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 2 * TN * 4; ++q) gelu2_formula<T>(w[q], g1[q], g2[q]);
+          }
+#pragma unroll
+          for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
+              const int q = 4 * jn + gq;
+              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(g1[2 * q], g1[2 * q + 1]);
+              *reinterpret_cast<uint2*>(row + kOut2 + c * 2) = make_uint2(g2[2 * q], g2[2 * q + 1]);
+            }
+        } else {
+#pragma unroll
+          for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
+              const int q = 4 * jn + gq;
+              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(w[2 * q], w[2 * q + 1]);
+            }
+        }
       }
       __syncthreads();
       if (storer) {
@@ -1119,6 +1156,8 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
             const uint32_t off =
                 (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
             store16(ro, off, *reinterpret_cast<const uint4*>(sp + rr * kPitch + ch * 16));
+            if constexpr (kGelu)
+              store16(ro2, off, *reinterpret_cast<const uint4*>(sp + kOut2 + rr * kPitch + ch * 16));
           }
         }
       }
@@ -1289,9 +1328,9 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   // every operand load, the others every output store (store_tile_split).
   constexpr bool kSplit = SPLIT;
   static_assert(!SPLIT || (NW == 8 && MODE != kDw && kDual != 1 &&
-                           (EPI == kEpiPlain || EPI == kEpiDualK) &&
+                           (EPI == kEpiPlain || EPI == kEpiDualK || EPI == kEpiGelu) &&
                            (WN / 32 == 2 || WN / 32 == 4)),
-                "split duties: 8-wave plain epilogues");
+                "split duties: 8-wave plain, two-part or GELU epilogues");
   constexpr int NL = kSplit ? NW / 2 : NW;  // waves that issue operand loads
   typedef StageLoader<BM, BN, kAK, kBKm, BK, NL, kDual> Loader;
   constexpr int kStage = Loader::TA::kBytes + Loader::kBBytes;
@@ -1536,8 +1575,9 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
       store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
       stores_out = kDrain && more;
     } else if constexpr (kSplit) {
-      static_assert(split_scratch_bytes<TN>(NW) <= kStage, "split scratch fits one stage");
-      store_tile_split<T, TM, TN, WGN, WM, WN, NW>(acc, job, wave, lane, smem + (NS - 1) * kStage);
+      static_assert(split_scratch_bytes<TN, EPI>(NW) <= kStage, "split scratch fits one stage");
+      store_tile_split<T, TM, TN, WGN, WM, WN, NW, EPI, kTab>(acc, job, wave, lane,
+                                                              smem + (NS - 1) * kStage, s_gtab);
     } else if constexpr (kLdsEpi) {
       // The ring's last slot is idle until the next tile's first iteration.
       static_assert(NW * epi_bytes<TN, kRows>() <= kStage, "epilogue scratch fits one stage");
@@ -2064,6 +2104,11 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
 // waves (measured: C4 +5%, C2 down-projection -10 us; shorter reductions and
 // the GELU epilogue were slower split).
 constexpr int64_t kSplitMinRed = 1024;
+// GELU forward with split duties only for long reductions (measured on
+// routed inputs, bit-identical either way: C4 up-projection, K = 4096,
+// 3885 -> 3840 us; C2, K = 512, 199 -> 282 us, where the short k-loop
+// cannot hide the storer waves' doubled store rounds).
+bool gelu_split(int64_t red) { return red >= 2048; }
 template <int MODE, int EPI>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t chunks = g.chunk > 0 ? g.E + g.A / g.chunk : g.E;
@@ -2080,6 +2125,10 @@ int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
       if constexpr (MODE != kDw && (EPI == kEpiPlain || EPI == kEpiDualK)) {
         const int64_t red = MODE == kFwd ? g.K : (EPI == kEpiDualK ? 2 * g.N : g.N);
         if (red >= kSplitMinRed)
+          return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2, true>(dtype, g, out_cols, s);
+      }
+      if constexpr (MODE == kFwd && EPI == kEpiGelu) {
+        if (gelu_split(g.K))
           return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2, true>(dtype, g, out_cols, s);
       }
       return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);

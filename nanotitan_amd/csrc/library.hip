@@ -1,6 +1,6 @@
 // Library-wide entry points: status messages, version, and the streaming
-// copy that measures the achievable HBM bandwidth the HBM-bound kernels are
-// graded against.
+// copy, fill and read that measure the achievable HBM bandwidth the
+// HBM-bound kernels are graded against.
 #include <algorithm>
 
 #include "common.hpp"
@@ -38,6 +38,41 @@ stream_copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64
   }
 }
 
+// Write-only and read-only counterparts of the copy (the ceilings of
+// kernels whose traffic is mostly writes, like the dispatch's k copies of
+// each row, or mostly reads): the same runs of kCopyUnroll vectors per lane.
+__global__ void __launch_bounds__(kCopyThreads)
+stream_fill_kernel(u32x4* __restrict__ dst, int64_t n, uint32_t value) {
+  constexpr int64_t kRun = (int64_t)kCopyThreads * kCopyUnroll;
+  const u32x4 v = {value, value, value, value};
+  for (int64_t base = (int64_t)blockIdx.x * kRun; base < n; base += (int64_t)gridDim.x * kRun) {
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = base + u * kCopyThreads + threadIdx.x;
+      if (i < n) dst[i] = v;
+    }
+  }
+}
+// Reads every vector and folds it into a per-lane XOR, stored only when it
+// equals `magic` (so the loads stay, and nothing is written in practice).
+__global__ void __launch_bounds__(kCopyThreads)
+stream_read_kernel(const u32x4* __restrict__ src, int64_t n, uint32_t magic,
+                   uint32_t* __restrict__ sink) {
+  constexpr int64_t kRun = (int64_t)kCopyThreads * kCopyUnroll;
+  uint32_t x = 0;
+  for (int64_t base = (int64_t)blockIdx.x * kRun; base < n; base += (int64_t)gridDim.x * kRun) {
+    u32x4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = base + u * kCopyThreads + threadIdx.x;
+      v[u] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) x ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  if (x == magic) sink[0] = x;
+}
+
 __global__ void byte_copy_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                  int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -67,6 +102,30 @@ int nt_stream_copy(void* dst, const void* src, size_t bytes, int32_t blocks, hip
                        dim3((unsigned)std::min<int64_t>(nt::ceil_div(tail, 256), 4096)), dim3(256),
                        0, stream, static_cast<const uint8_t*>(src) + n16 * 16,
                        static_cast<uint8_t*>(dst) + n16 * 16, tail);
+  return nt::launch_status();
+}
+
+int nt_stream_fill(void* dst, size_t bytes, uint32_t value, hipStream_t stream) {
+  if (bytes == 0) return NT_OK;
+  if (dst == nullptr || reinterpret_cast<uintptr_t>(dst) % 16 != 0 || bytes % 16 != 0)
+    return NT_ERR_INVALID_ARG;
+  const int64_t n16 = (int64_t)(bytes / 16);
+  const int64_t runs = nt::ceil_div(n16, (int64_t)nt::kCopyThreads * nt::kCopyUnroll);
+  hipLaunchKernelGGL(nt::stream_fill_kernel, dim3((unsigned)std::min<int64_t>(runs, 8192)),
+                     dim3(nt::kCopyThreads), 0, stream, static_cast<nt::u32x4*>(dst), n16, value);
+  return nt::launch_status();
+}
+
+int nt_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream) {
+  if (bytes == 0) return NT_OK;
+  if (src == nullptr || sink == nullptr || reinterpret_cast<uintptr_t>(src) % 16 != 0 ||
+      bytes % 16 != 0)
+    return NT_ERR_INVALID_ARG;
+  const int64_t n16 = (int64_t)(bytes / 16);
+  const int64_t runs = nt::ceil_div(n16, (int64_t)nt::kCopyThreads * nt::kCopyUnroll);
+  hipLaunchKernelGGL(nt::stream_read_kernel, dim3((unsigned)std::min<int64_t>(runs, 8192)),
+                     dim3(nt::kCopyThreads), 0, stream, static_cast<const nt::u32x4*>(src), n16,
+                     0x9E3779B9u, sink);
   return nt::launch_status();
 }
 

@@ -770,6 +770,28 @@ void stream_copy(Tensor dst, Tensor src, int64_t blocks) {
                "stream_copy");
 }
 
+// stream_fill(dst, value) / stream_read(src, sink): the write-only and
+// read-only bandwidth references (sink: one int32 on src's device).
+void stream_fill(Tensor dst, int64_t value) {
+  check_device(dst, "dst");
+  TORCH_CHECK(dst.is_contiguous(), "dst must be contiguous");
+  c10::hip::HIPGuard guard(dst.get_device());
+  check_status(nt_stream_fill(dst.data_ptr(), (size_t)dst.numel() * dst.element_size(),
+                              (uint32_t)value, stream_of(dst)),
+               "stream_fill");
+}
+void stream_read(Tensor src, Tensor sink) {
+  check_device(src, "src");
+  check_device(sink, "sink");
+  TORCH_CHECK(src.is_contiguous() && sink.numel() >= 1 && sink.element_size() == 4,
+              "src must be contiguous and sink one 32-bit word");
+  check_same_device(src, {&sink});
+  c10::hip::HIPGuard guard(src.get_device());
+  check_status(nt_stream_read(src.data_ptr(), (size_t)src.numel() * src.element_size(),
+                              static_cast<uint32_t*>(sink.data_ptr()), stream_of(src)),
+               "stream_read");
+}
+
 // ------------------------------------------------------------ Meta kernels
 //
 // Output shapes and dtypes only (fake / meta tensors, torch.compile tracing):
@@ -1064,6 +1086,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dispatch_tokens_counted", &dispatch_tokens_counted,
         "dispatch_tokens from the counts route_topk_count computed");
   m.def("route_topk_backward", &route_topk_backward, "Gradient of route_topk's gates -> dlogits");
+  m.def("stream_fill", &stream_fill, "16-byte streaming device fill (write bandwidth reference)",
+        pybind11::arg("dst"), pybind11::arg("value") = 0);
+  m.def("stream_read", &stream_read, "16-byte streaming device read (read bandwidth reference)",
+        pybind11::arg("src"), pybind11::arg("sink"));
   m.def("stream_copy", &stream_copy, "16-byte streaming device copy (bandwidth reference)",
         pybind11::arg("dst"), pybind11::arg("src"), pybind11::arg("blocks") = 0);
   m.def("version", []() { return nt_version(); });
