@@ -312,3 +312,71 @@ def test_route_dispatch_fn_no_tokens(ext):
     assert X.grad.shape == (0, 16) and Z.grad.shape == (0, 8)
     dX, dl = ext.pack_backward_inv_route(px.detach(), pw.detach(), inv, gates.detach(), idx, 8)
     assert dX.shape == (0, 16) and dl.shape == (0, 8)
+
+
+def test_moe_module_expert_grads_bf16_rounded_restatement(ext):
+    """The SwiGLU expert weights' gradients of MoE(cfg) within bf16 2e-2
+    against a float64 restatement that rounds to bf16 every tensor the
+    reference's unfused bf16 graph stores (src/model/feed_fwd.py:107-112 and
+    its autograd; src/model/cuda_backend.py:69-75): gate and value (GEMM
+    outputs), silu(gate), hidden, the expert outputs, the layer output
+    (combined in fp32, then cast), and backward dY, each expert output's
+    gradient dY * gate, dhidden (a GEMM output), dvalue = dhidden * silu(gate),
+    dhidden * value and dgate = that * silu'(gate); the weight gradients are
+    fp32 sums rounded once. Routing and gates come from the same float64
+    router as the layer's."""
+    from nanotitan_amd.layer import MoE
+
+    bf = torch.bfloat16
+
+    def rnd(t):
+        return t.to(bf).double()
+
+    cfg = SimpleNamespace(d_model=64, num_experts=16, top_k=4, ffn_in=128, dtype=bf,
+                          moe_router_dtype=torch.float32, moe_backend="hip", router_alpha=0.01)
+    torch.manual_seed(21)
+    moe = MoE(cfg).cuda()
+    g = torch.Generator().manual_seed(22)
+    B, S, d, E, k = 4, 32, cfg.d_model, cfg.num_experts, cfg.top_k
+    x_cpu = torch.randn(B, S, d, generator=g).to(bf)
+    x = x_cpu.cuda().requires_grad_(True)
+    y, stats = moe(x)
+    y.float().square().mean().backward()
+    torch.cuda.synchronize()
+
+    Wr = moe.router.weight.detach().cpu().double()
+    Wg, Wv, Wo = (p.detach().cpu().double() for p in
+                  (moe.experts.W_gate, moe.experts.W_val, moe.experts.W_out))
+    flat = x_cpu.double().reshape(-1, d)
+    T = flat.shape[0]
+    logits = flat @ Wr.T
+    idx = O.select_topk(logits.float(), k)
+    gates = logits.gather(1, idx).softmax(-1).float().double()  # fp32 gates
+    # forward, one (token, slot) assignment per row
+    xa = flat.repeat_interleave(k, 0)                      # [T*k, d]
+    ea = idx.reshape(-1)
+    gate = rnd(torch.einsum("ad,adf->af", xa, Wg[ea]))
+    val = rnd(torch.einsum("ad,adf->af", xa, Wv[ea]))
+    sg = rnd(torch.nn.functional.silu(gate))
+    hid = rnd(sg * val)
+    ye = rnd(torch.einsum("af,afd->ad", hid, Wo[ea]))
+    out = (gates.reshape(-1, 1) * ye).reshape(T, k, d).sum(1)
+    y_ref = rnd(out)
+    # backward of mean(y^2): dY rounded to bf16 where autograd casts it back
+    dY = rnd(2.0 * y_ref / y_ref.numel())
+    dye = rnd(dY.repeat_interleave(k, 0) * gates.reshape(-1, 1))
+    dhid = rnd(torch.einsum("ad,afd->af", dye, Wo[ea]))
+    dval = rnd(dhid * sg)
+    dsg = rnd(dhid * val)
+    s = torch.sigmoid(gate)
+    dgate = rnd(dsg * s * (1 + gate * (1 - s)))
+    dWg = torch.zeros_like(Wg)
+    dWv = torch.zeros_like(Wv)
+    dWo = torch.zeros_like(Wo)
+    dWg.index_add_(0, ea, torch.einsum("ad,af->adf", xa, dgate))
+    dWv.index_add_(0, ea, torch.einsum("ad,af->adf", xa, dval))
+    dWo.index_add_(0, ea, torch.einsum("af,ad->afd", hid, dye))
+    _close_rms(y, y_ref.reshape(B, S, d))
+    _close_rms(moe.experts.W_gate.grad, rnd(dWg), rtol=2e-2)
+    _close_rms(moe.experts.W_val.grad, rnd(dWv), rtol=2e-2)
+    _close_rms(moe.experts.W_out.grad, rnd(dWo), rtol=2e-2)

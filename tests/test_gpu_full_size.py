@@ -277,3 +277,49 @@ def test_c5_boundary_ties_full_size_bit_exact_and_repeatable(ext):
     torch.testing.assert_close(out16[S].float(), ref_out.float(), rtol=2e-2, atol=2e-2)
     torch.testing.assert_close(runs[0][1].view(c.dtype)[S].float(), ref["x"].float(), rtol=2e-2,
                                atol=2e-2)
+
+
+@pytest.mark.parametrize("cfg_id", [4, 5])
+def test_dispatch_full_width_bit_exact(ext, cfg_id):
+    """The dispatch at C4 and C5 in full: every token at its real row width
+    (4096 bf16 / 2048 fp16 columns, the long-row pack kernel), through the
+    layer's path (router with fused count, counted dispatch) and the plain
+    dispatch. Bit for bit over all rows: counts = bincount, offsets = their
+    exclusive scan, token_id / expert / inv = the oracle's stable counting
+    sort (the permutation alone: the oracle gets one column), packed rows
+    = torch's gather X[token_id] on the GPU, packed gates = w[t, slot], and
+    token_id / inv inverse maps of each other."""
+    import numpy as np
+
+    d = O.make_inputs(cfg_id, with_weights=False)
+    c = d["cfg"]
+    X = d["X"].to(c.dtype)
+    T, k, E = X.shape[0], c.k, c.E
+    print(f"[full-width dispatch] C{cfg_id} T={T} d={X.shape[1]} E={E} k={k}", flush=True)
+    want_g, want_i, _ = O.route(d["logits"], k)
+    counts, offsets, p = O.dispatch(X[:, :1].contiguous(), want_g, want_i, E)
+    Xg = X.cuda()
+    g, i, ws = ext.route_topk_count(d["logits"].cuda(), k, Xg)
+    assert torch.equal(i.cpu(), want_i)
+    runs = {"counted": ext.dispatch_tokens_counted(Xg, g, i, E, ws),
+            "plain": ext.dispatch_tokens(Xg, g, i, E)}
+    for name, (g_counts, g_off, g_px, g_tid, g_ex, g_pw, g_inv) in runs.items():
+        torch.cuda.synchronize()
+        assert np.array_equal(g_counts.cpu().numpy(), counts), name
+        assert np.array_equal(g_off.cpu().numpy(), offsets), name
+        assert np.array_equal(g_tid.cpu().numpy(), p.token_id), name
+        assert np.array_equal(g_ex.cpu().numpy(), p.expert), name
+        assert np.array_equal(g_inv.cpu().numpy(), p.inv), name
+        A = T * k
+        assert g_px.shape == (A, X.shape[1])
+        gathered = Xg.index_select(0, g_tid.long())
+        assert torch.equal(g_px.view(torch.int16), gathered.view(torch.int16)), name
+        del gathered
+        flat_inv = g_inv.reshape(-1).long()
+        assert torch.equal(g_pw[flat_inv], g.reshape(-1)), name  # gate of assignment (t, j)
+        t_of = torch.arange(T, device="cuda").repeat_interleave(k)
+        assert torch.equal(g_tid[flat_inv].long(), t_of), name  # token_id o inv = identity
+        assert torch.equal(g_ex[flat_inv], i.reshape(-1)), name
+        assert torch.equal(torch.sort(flat_inv).values, torch.arange(A, device="cuda")), name
+    del runs
+    torch.cuda.empty_cache()
