@@ -1007,6 +1007,14 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
             *reinterpret_cast<uint2*>(scratch + (r % ROWS) * kPitch + c * 2) = pk;
           }
       }
+      // Each lane reads back rows other lanes wrote. The compiler models
+      // lanes as threads, so without a fence it may forward a lane's earlier
+      // read of the same scratch address where that lane wrote nothing: with
+      // 16-row passes it moved the second pass's reads into the writing
+      // lanes' branch, and the other lanes stored the first pass's rows
+      // again. A wavefront-scope fence emits no instruction (a wave's LDS
+      // operations complete in order) and forbids that.
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       auto chunk_off = [&](int q, uint4& v) -> uint32_t {
         const int rr = q * kRowsPerRead + lane / kLanesPerRow;
         const int ch = lane % kLanesPerRow;
