@@ -933,7 +933,8 @@ __device__ __forceinline__ void epilogue8(uint4 v, __amdgpu_buffer_rsrc_t ro,
 // banks), and read back 16 bytes per lane so that every store instruction
 // writes whole 128- or 256-byte row segments. `scratch` is
 // epi_bytes<TN, ROWS>() bytes private to the wave; LDS operations of one
-// wave complete in order, so no barrier is needed. With ROWS = 16 the
+// wave complete in order, so no barrier is needed (a wavefront fence keeps
+// the compiler from reusing a lane's earlier reads). With ROWS = 16 the
 // sub-tile goes through in two halves (lanes 0-15 and 32-47 hold rows 0-15,
 // the others rows 16-31), halving the scratch.
 template <int TN>
@@ -1324,8 +1325,9 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   constexpr int TM = WM / 32, TN = WN / 32;
   static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
   static_assert(NS >= 2, "at least two LDS stages");
-  // Only the 64-deep k-step is built and tested: a 32-deep variant (measured
-  // at C3 and C4, slower) gave results that differ from it.
+  // Only the 64-deep k-step is built and tested: 32-deep k-steps with 2 to 4
+  // stages give the same bits (measured on MI355X) but were 7-13% slower at
+  // C4 and slower at C3.
   static_assert(BK == 64, "k-step depth 64");
   constexpr bool kAK = MODE != kDw;   // A operand K-major?
   constexpr bool kBKm = MODE == kDx;  // B operand K-major?
