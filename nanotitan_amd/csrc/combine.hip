@@ -69,27 +69,15 @@ __device__ __forceinline__ void unpack_vec(raw_vec<T, VE> w, float (&out)[VE]) {
   for (int i = 0; i < VE; ++i) out[i] = elem<T>::load(v.v[i]);
 }
 
-// One gathered row chunk of a wave's k rows: the raw word (RAW) or floats.
-// Raw words halve the registers of 16-bit rows, which keeps the k = 8
-// gathers and the short rows at full occupancy; with k <= 2 and long rows
-// the float form was faster (measured cold at C4: combine 75 vs 78 us).
-template <typename T, int VE, bool RAW>
-struct RowBuf;
-template <typename T, int VE>
-struct RowBuf<T, VE, true> {
-  raw_vec<T, VE> w;
-  __device__ void load(const typename elem<T>::storage* p) { w = load_raw<T, VE>(p); }
-  __device__ void get(float (&out)[VE]) const { unpack_vec<T, VE>(w, out); }
-};
-template <typename T, int VE>
-struct RowBuf<T, VE, false> {
-  float f[VE];
-  __device__ void load(const typename elem<T>::storage* p) { load_vec<T, VE>(p, f); }
-  __device__ void get(float (&out)[VE]) const {
-#pragma unroll
-    for (int v = 0; v < VE; ++v) out[v] = f[v];
-  }
-};
+// The small-fan-in gathers issue every row load of a pass before the first
+// is used, then wait once for all of them (wait_batch_loads, a scheduling
+// fence and a full wait): without the fence the compiler converts each row
+// as it arrives and waits for it before issuing the next load, so a wave
+// kept one row chunk in flight.
+// A pass covers H consecutive 16-byte-per-lane chunks of each row: rows of
+// several chunks (k <= 2) take kLongChunks per pass; a chunk beyond the row
+// loads the pass's first chunk again and is discarded.
+constexpr int kLongChunks = 4;
 
 template <typename T, int VE>
 __device__ __forceinline__ void store_vec(typename elem<T>::storage* p, const float (&in)[VE]) {
@@ -438,10 +426,29 @@ __device__ __forceinline__ void sorted_slots(const int32_t* __restrict__ inv, in
         p[u][j] = a < b ? a : b;
         p[u][j + 1] = a < b ? b : a;
       }
+    // Every lane computed the same slots from the same broadcasts: moving
+    // them to scalar registers makes the row loads' conditions uniform, so
+    // the loads are issued back to back instead of one per branch.
+    n[u] = __builtin_amdgcn_readfirstlane(n[u]);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) p[u][j] = __builtin_amdgcn_readfirstlane(p[u][j]);
   }
 }
 
-template <typename T, typename TO, int VE, int KMAX, int U, bool RAW>
+// A row every lane may load for a slot that has none: the first valid slot
+// of the wave's tokens (-1 when none has one). Loading it for the empty
+// slots lets every row load of a pass be issued unconditionally, back to
+// back; the empty slots' data is never used.
+template <int KMAX, int U>
+__device__ __forceinline__ int32_t fill_row(const int32_t (&p)[U][KMAX], const int (&n)[U]) {
+  int32_t r = -1;
+#pragma unroll
+  for (int u = U - 1; u >= 0; --u)
+    if (n[u] > 0) r = p[u][0];
+  return r;
+}
+
+template <typename T, typename TO, int VE, int KMAX, int U, int H>
 __global__ void __launch_bounds__(kThreads)
 combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
                    const int32_t* __restrict__ inv, int32_t k, const float* __restrict__ w,
@@ -458,31 +465,45 @@ combine_inv_kernel(const typename elem<T>::storage* __restrict__ y,
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) wp[u][j] = j < n[u] ? w[p[u][j]] : 0.f;
-  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
-    RowBuf<T, VE, RAW> x[U][KMAX];
+  const int32_t fill = fill_row<KMAX, U>(p, n);
+  constexpr int64_t kStep = (int64_t)kWave * VE;
+  for (int64_t h0 = (int64_t)lane * VE; h0 < d; h0 += H * kStep) {
+    raw_vec<T, VE> x[H][U][KMAX];
+    if (fill >= 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int c = 0; c < H; ++c) {
+        const int64_t hl = h0 + c * kStep < d ? h0 + c * kStep : h0;
 #pragma unroll
-      for (int j = 0; j < KMAX; ++j)
-        if (j < n[u]) x[u][j].load(y + (int64_t)p[u][j] * d + h);
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (t0 + u >= T_) break;
-      float acc[VE];
+          for (int j = 0; j < KMAX; ++j)
+            x[c][u][j] = load_raw<T, VE>(y + (int64_t)(j < n[u] ? p[u][j] : fill) * d + hl);
+      }
+    }
+    wait_batch_loads();
 #pragma unroll
-      for (int v = 0; v < VE; ++v) acc[v] = 0.f;
-      {
+    for (int c = 0; c < H; ++c) {
+      const int64_t h = h0 + c * kStep;
+      if (h >= d) break;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t0 + u >= T_) break;
+        float acc[VE];
+#pragma unroll
+        for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+        {
 #pragma clang fp contract(off)
 #pragma unroll
-        for (int j = 0; j < KMAX; ++j)
-          if (j < n[u]) {
-            float xf[VE];
-            x[u][j].get(xf);
+          for (int j = 0; j < KMAX; ++j)
+            if (j < n[u]) {
+              float xf[VE];
+              unpack_vec<T, VE>(x[c][u][j], xf);
 #pragma unroll
-            for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp[u][j] * xf[v];
-          }
+              for (int v = 0; v < VE; ++v) acc[v] = acc[v] + wp[u][j] * xf[v];
+            }
+        }
+        store_vec<TO, VE>(out + (t0 + u) * d + h, acc);
       }
-      store_vec<TO, VE>(out + (t0 + u) * d + h, acc);
     }
   }
 }
@@ -527,49 +548,77 @@ combine_bwd_kernel(const typename elem<T>::storage* __restrict__ y,
 
 // Inverse-map form, one wave per token: the dY row is read once and serves
 // all k packed rows of the token. Same per-row arithmetic and reduction
-// order as combine_bwd_kernel, so dw and dy are bit-identical to it.
-template <typename T, typename TG, int VE, int KB>
+// order as combine_bwd_kernel, so dw and dy are bit-identical to it. The
+// block's slots are read by one load and held in scalar registers, and every
+// row load of a pass is issued before the first is used (an empty slot
+// loads the block's first valid row and discards it).
+template <typename T, typename TG, int VE, int KB, int H>
 __global__ void __launch_bounds__(kThreads)
 combine_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ y,
                        const int32_t* __restrict__ inv, const float* __restrict__ w,
                        const typename elem<TG>::storage* __restrict__ dY, int64_t T_, int32_t k,
                        int64_t d, typename elem<T>::storage* __restrict__ dy,
                        float* __restrict__ dw) {
-  const int wave = threadIdx.x / kWave;
+  static_assert(KB <= kWave, "a block's slots fit one wave");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = lane_id();
   const int64_t t = (int64_t)blockIdx.x * kWaves + wave;
   if (t >= T_) return;
+  const int64_t rows = T_ * k;
   for (int j0 = 0; j0 < k; j0 += KB) {
     const int nj = min(KB, k - j0);
+    int32_t mine = lane < nj ? inv[t * k + j0 + lane] : -1;
+    if (mine >= rows) mine = -1;
+    const float wmine = mine >= 0 ? w[mine] : 0.f;
     int32_t pj[KB];
     float wj[KB], part[KB];
+    int32_t fill = -1;
 #pragma unroll
-    for (int j = 0; j < KB; ++j) {
-      pj[j] = j < nj ? inv[t * k + j0 + j] : -1;
-      if (pj[j] >= T_ * k) pj[j] = -1;
-      wj[j] = pj[j] >= 0 ? w[pj[j]] : 0.f;
+    for (int j = KB - 1; j >= 0; --j) {
+      pj[j] = __builtin_amdgcn_readlane(mine, j);
+      wj[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wmine), j));
       part[j] = 0.f;
+      if (pj[j] >= 0) fill = pj[j];
     }
-    for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
-      float g[VE];
-      load_vec<TG, VE>(dY + t * d + h, g);
+    if (fill < 0) continue;  // no valid slot in this block
+    constexpr int64_t kStep = (int64_t)kWave * VE;
+    for (int64_t h0 = (int64_t)lane * VE; h0 < d; h0 += H * kStep) {
+      raw_vec<TG, VE> gw[H];
+      raw_vec<T, VE> xw[H][KB];
 #pragma unroll
-      for (int j = 0; j < KB; ++j) {
-        if (pj[j] < 0) continue;
-        float x[VE], o[VE];
-        load_vec<T, VE>(y + (int64_t)pj[j] * d + h, x);
+      for (int c = 0; c < H; ++c) {
+        const int64_t hl = h0 + c * kStep < d ? h0 + c * kStep : h0;
+        gw[c] = load_raw<TG, VE>(dY + t * d + hl);
 #pragma unroll
-        for (int v = 0; v < VE; ++v) {
-          o[v] = __fmul_rn(g[v], wj[j]);
-          part[j] = fmaf(g[v], x[v], part[j]);
+        for (int j = 0; j < KB; ++j)
+          xw[c][j] = load_raw<T, VE>(y + (int64_t)(pj[j] >= 0 ? pj[j] : fill) * d + hl);
+      }
+      wait_batch_loads();
+#pragma unroll
+      for (int c = 0; c < H; ++c) {
+        const int64_t h = h0 + c * kStep;
+        if (h >= d) break;
+        float g[VE];
+        unpack_vec<TG, VE>(gw[c], g);
+        // Every slot sums (an empty one its discarded fill row), so no row
+        // load is moved behind a slot's condition; only the stores test it.
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+          float x[VE], o[VE];
+          unpack_vec<T, VE>(xw[c][j], x);
+#pragma unroll
+          for (int v = 0; v < VE; ++v) {
+            o[v] = __fmul_rn(g[v], wj[j]);
+            part[j] = fmaf(g[v], x[v], part[j]);
+          }
+          if (pj[j] >= 0) store_vec<T, VE>(dy + (int64_t)pj[j] * d + h, o);
         }
-        store_vec<T, VE>(dy + (int64_t)pj[j] * d + h, o);
       }
     }
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
-      const float s = wave_sum(part[j]);
-      if (lane == 0 && pj[j] >= 0) dw[pj[j]] = s;
+      const float sum = wave_sum(part[j]);
+      if (lane == 0 && pj[j] >= 0) dw[pj[j]] = sum;
     }
   }
 }
@@ -679,7 +728,7 @@ __device__ __forceinline__ void route_grad_row(const RouteGrad& rg, int64_t t, b
 // (ascending packed order, fp32), U tokens per wave with every row load
 // issued up front. dw may be null (not written); rg.dlogits non-null adds
 // the router's backward (route_grad_row).
-template <typename T, int VE, int KMAX, int U, bool RAW>
+template <typename T, int VE, int KMAX, int U, int H>
 __global__ void __launch_bounds__(kThreads)
 pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
                     const float* __restrict__ dpw, const int32_t* __restrict__ inv,
@@ -701,28 +750,42 @@ pack_bwd_inv_kernel(const typename elem<T>::storage* __restrict__ dpX,
     if (dw != nullptr && jl < k && tl < T_) dw[tl * k + jl] = dg;
     if (rg.dlogits != nullptr) route_grad_row(rg, tl, tl < T_, k, jl, kSeg, dg);
   }
-  for (int64_t h = (int64_t)lane * VE; h < d; h += (int64_t)kWave * VE) {
-    RowBuf<T, VE, RAW> x[U][KMAX];
+  const int32_t fill = fill_row<KMAX, U>(p, n);
+  constexpr int64_t kStep = (int64_t)kWave * VE;
+  for (int64_t h0 = (int64_t)lane * VE; h0 < d; h0 += H * kStep) {
+    raw_vec<T, VE> x[H][U][KMAX];
+    if (fill >= 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int c = 0; c < H; ++c) {
+        const int64_t hl = h0 + c * kStep < d ? h0 + c * kStep : h0;
 #pragma unroll
-      for (int j = 0; j < KMAX; ++j)
-        if (j < n[u]) x[u][j].load(dpX + (int64_t)p[u][j] * d + h);
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (t0 + u >= T_) break;
-      float acc[VE];
+          for (int j = 0; j < KMAX; ++j)
+            x[c][u][j] = load_raw<T, VE>(dpX + (int64_t)(j < n[u] ? p[u][j] : fill) * d + hl);
+      }
+    }
+    wait_batch_loads();
 #pragma unroll
-      for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+    for (int c = 0; c < H; ++c) {
+      const int64_t h = h0 + c * kStep;
+      if (h >= d) break;
 #pragma unroll
-      for (int j = 0; j < KMAX; ++j)
-        if (j < n[u]) {
-          float xf[VE];
-          x[u][j].get(xf);
+      for (int u = 0; u < U; ++u) {
+        if (t0 + u >= T_) break;
+        float acc[VE];
 #pragma unroll
-          for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], xf[v]);
-        }
-      store_vec<T, VE>(dX + (t0 + u) * d + h, acc);
+        for (int v = 0; v < VE; ++v) acc[v] = 0.f;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+          if (j < n[u]) {
+            float xf[VE];
+            unpack_vec<T, VE>(x[c][u][j], xf);
+#pragma unroll
+            for (int v = 0; v < VE; ++v) acc[v] = __fadd_rn(acc[v], xf[v]);
+          }
+        store_vec<T, VE>(dX + (t0 + u) * d + h, acc);
+      }
     }
   }
 }
@@ -756,9 +819,9 @@ int run_combine(const void* y, ListSrc src, const float* w, int64_t T_, int64_t 
 #define NT_CI(VE, KM) \
   do {                                                                                   \
     if (KM <= 2 && long_rows)                                                            \
-      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), false>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
+      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), kLongChunks>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
     else                                                                                 \
-      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), true>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
+      hipLaunchKernelGGL((combine_inv_kernel<T, TO, VE, KM, fan_u(KM, kCombineU), 1>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, kCombineU))), dim3(kThreads), 0, s, yp, src.list, src.k, w, T_, d, op); \
   } while (0)
 #define NT_CI_VE(KM)            \
   switch (ve) {                 \
@@ -839,31 +902,39 @@ int run_combine_bwd_inv(const void* y, const int32_t* inv, const float* w, const
   const S* yp = static_cast<const S*>(y);
   const SG* gp = static_cast<const SG*>(dY);
   S* dyp = static_cast<S*>(dy);
-#define NT_CBI(VE, KB) \
-  hipLaunchKernelGGL((combine_bwd_inv_kernel<T, TG, VE, KB>), grid, dim3(kThreads), 0, s, yp, inv, w, gp, T_, k, d, dyp, dw)
-  if (k <= 2) {
+#define NT_CBI(VE, KB, H) \
+  hipLaunchKernelGGL((combine_bwd_inv_kernel<T, TG, VE, KB, H>), grid, dim3(kThreads), 0, s, yp, inv, w, gp, T_, k, d, dyp, dw)
+  const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
+  if (k <= 2 && long_rows) {
     switch (ve) {
-      case 8: NT_CBI(8, 2); break;
-      case 4: NT_CBI(4, 2); break;
-      case 2: NT_CBI(2, 2); break;
-      default: NT_CBI(1, 2); break;
+      case 8: NT_CBI(8, 2, kLongChunks); break;
+      case 4: NT_CBI(4, 2, kLongChunks); break;
+      case 2: NT_CBI(2, 2, kLongChunks); break;
+      default: NT_CBI(1, 2, kLongChunks); break;
     }
-  } else if (d * (int64_t)sizeof(S) > kLongRowBytes) {
+  } else if (k <= 2) {
     switch (ve) {
-      case 8: NT_CBI(8, 8); break;
-      case 4: NT_CBI(4, 8); break;
-      case 2: NT_CBI(2, 8); break;
-      default: NT_CBI(1, 8); break;
+      case 8: NT_CBI(8, 2, 1); break;
+      case 4: NT_CBI(4, 2, 1); break;
+      case 2: NT_CBI(2, 2, 1); break;
+      default: NT_CBI(1, 2, 1); break;
+    }
+  } else if (long_rows) {
+    switch (ve) {
+      case 8: NT_CBI(8, 8, 1); break;
+      case 4: NT_CBI(4, 8, 1); break;
+      case 2: NT_CBI(2, 8, 1); break;
+      default: NT_CBI(1, 8, 1); break;
     }
   } else {
     // Short rows, k > 2: four rows per pass over dY (a second pass re-reads
     // the token's dY row from L2) keeps the kernel at 71 registers instead
     // of 95 (measured cold, C3: 126 -> 108 us; long rows were 5% slower so).
     switch (ve) {
-      case 8: NT_CBI(8, 4); break;
-      case 4: NT_CBI(4, 4); break;
-      case 2: NT_CBI(2, 4); break;
-      default: NT_CBI(1, 4); break;
+      case 8: NT_CBI(8, 4, 1); break;
+      case 4: NT_CBI(4, 4, 1); break;
+      case 2: NT_CBI(2, 4, 1); break;
+      default: NT_CBI(1, 4, 1); break;
     }
   }
 #undef NT_CBI
@@ -882,13 +953,13 @@ int run_pack_bwd(const void* dpX, const float* dpw, ListSrc src, const int32_t* 
   S* op = static_cast<S*>(dX);
   if (src.start == nullptr && expert == nullptr && k <= 8) {
     const bool long_rows = d * (int64_t)sizeof(S) > kLongRowBytes;
-#define NT_PBI_U(VE, KM, U, RAW) \
-  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U), RAW>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw, rg)
-#define NT_PBI(VE, KM)                                                    \
-  do {                                                                    \
-    if (long_rows && KM <= 2) NT_PBI_U(VE, KM, kPackBwdULong, false);     \
-    else if (long_rows) NT_PBI_U(VE, KM, kPackBwdULong, true);            \
-    else NT_PBI_U(VE, KM, kPackBwdU, true);                               \
+#define NT_PBI_U(VE, KM, U, H) \
+  hipLaunchKernelGGL((pack_bwd_inv_kernel<T, VE, KM, fan_u(KM, U), H>), dim3((unsigned)ceil_div(T_, kWaves * fan_u(KM, U))), dim3(kThreads), 0, s, ip, dpw, src.list, T_, k, d, op, dw, rg)
+#define NT_PBI(VE, KM)                                                      \
+  do {                                                                      \
+    if (long_rows && KM <= 2) NT_PBI_U(VE, KM, kPackBwdULong, kLongChunks); \
+    else if (long_rows) NT_PBI_U(VE, KM, kPackBwdULong, 1);                 \
+    else NT_PBI_U(VE, KM, kPackBwdU, 1);                                    \
   } while (0)
 #define NT_PBI_VE(KM)            \
   switch (ve) {                  \

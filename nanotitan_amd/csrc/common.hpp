@@ -171,6 +171,18 @@ __device__ __forceinline__ void lds_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// Scheduling fence, then s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at
+// their gfx9 maxima): every vector memory operation the wave has issued has
+// completed. The gathers and copies issue a batch of loads, call this once,
+// and then store with no further wait: the compiler, unsure whether the
+// stores under uniform branches were issued, would otherwise wait for a
+// count that includes them before each next group of stores. A real wait
+// instruction, so the compiler's own wait insertion accounts for it.
+__device__ __forceinline__ void wait_batch_loads() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xF70);
+}
+
 // One round of a workgroup-wide stable counting rank. Every thread of the
 // workgroup passes one item (key in [0, nkeys) when valid); the result is the
 // number of valid items with the same key that precede it in thread order in

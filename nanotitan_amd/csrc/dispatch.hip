@@ -132,6 +132,41 @@ __device__ __forceinline__ void copy_row_to_slots(const V* __restrict__ src, V* 
   }
 }
 
+// The same copy for 16-byte vectors and k <= kSlotRegs: the token's slots
+// are read once into scalar registers, every load of a batch of LB vectors
+// per lane is issued before the first store (a vector beyond the row loads
+// the batch's first again and is not stored), and one wait covers the batch
+// (wait_batch_loads). Before, the stores of each vector waited for those of
+// the one before (the wait count also covers stores).
+constexpr int kSlotRegs = 8;
+
+template <typename V, int LB>
+__device__ __forceinline__ void copy_row_to_slot_regs(const V* __restrict__ src,
+                                                      V* __restrict__ dst, int64_t nv,
+                                                      const int32_t* slots, int k) {
+  int32_t ps[kSlotRegs];
+#pragma unroll
+  for (int j = 0; j < kSlotRegs; ++j) ps[j] = j < k ? __builtin_amdgcn_readfirstlane(slots[j]) : -1;
+  const int lane = lane_id();
+  for (int64_t c0 = lane; c0 < nv; c0 += (int64_t)kWave * LB) {
+    V v[LB];
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int64_t c = c0 + (int64_t)u * kWave;
+      v[u] = load_nt(src + (c < nv ? c : c0));  // each token row is read once
+    }
+    wait_batch_loads();
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      const int64_t c = c0 + (int64_t)u * kWave;
+      if (c >= nv) break;
+#pragma unroll
+      for (int j = 0; j < kSlotRegs; ++j)
+        if (ps[j] >= 0) dst[(int64_t)ps[j] * nv + c] = v[u];
+    }
+  }
+}
+
 constexpr int kRowBatch = 16;  // rows in flight per wave in the short-row copy
 
 // Rank, place and copy. base_mode 0: base[e] comes from `base` (cursor copy);
@@ -322,6 +357,18 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
       }
       return;
     }
+  }
+  if (sizeof(V) == 16 && k <= kSlotRegs) {
+    // 8 vectors per lane per batch from rows of 8 KiB, 4 below (one batch
+    // covers a 4 KiB row)
+    for (int t = wave; t < ntok; t += kDispatchWaves) {
+      if (nv >= (int64_t)kWave * kLongRowBatch)
+        copy_row_to_slot_regs<V, kLongRowBatch>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);
+      else
+        copy_row_to_slot_regs<V, kLongRowBatch / 2>(X + (tok0 + t) * nv, packed_X, nv,
+                                                     s_pos + t * k, k);
+    }
+    return;
   }
   for (int t = wave; t < ntok; t += kDispatchWaves) {
     copy_row_to_slots<V>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);

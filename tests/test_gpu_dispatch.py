@@ -96,6 +96,33 @@ def test_pack_tokens_random_vs_oracle(ext, dtype, T, k, E, d):
     assert torch.equal(bits(px), bits(p.packed_X))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,k,E,d", [(300, 1, 13, 1000), (300, 3, 13, 1000), (200, 8, 40, 4104),
+                                     (150, 2, 8, 4104), (100, 9, 16, 1000)])
+def test_pack_tokens_long_rows_vs_oracle(ext, dtype, T, k, E, d):
+    """Rows longer than one 16-byte vector per lane (the batched long-row
+    copy): rows that end inside a batch (1000 and 4104 elements), k on both
+    sides of the copy's register-slot limit (8), and out-of-range expert ids
+    (their slots are skipped)."""
+    g = torch.Generator().manual_seed(T * 11 + k + d)
+    X = torch.randn(T, d, generator=g).to(dtype)
+    w = torch.rand(T, k, generator=g)
+    topk = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    topk[torch.rand(T, k, generator=g) < 0.05] = E + 3
+    counts = O.count_experts(topk, None, E)
+    cursor = O.offsets_from_counts(counts)
+    p = O.pack_tokens(X, w, topk, cursor)
+    cur_g = torch.from_numpy(cursor).cuda()
+    px, tid, ex, pw, inv = ext.pack_tokens_inv(X.cuda(), w.cuda(), topk.cuda(), cur_g)
+    torch.cuda.synchronize()
+    n = int(counts.sum())  # the valid assignments fill slots [0, n)
+    assert p.written[:n].all() and not p.written[n:].any()
+    assert np.array_equal(cur_g.cpu().numpy(), p.cursor_after)
+    assert np.array_equal(inv.cpu().numpy(), p.inv)
+    assert np.array_equal(tid.cpu().numpy()[:n], p.token_id[:n])
+    assert torch.equal(bits(px[:n]), bits(p.packed_X[:n]))
+
+
 def test_count_with_mask(ext):
     g = torch.Generator().manual_seed(11)
     topk = torch.randint(0, 16, (5000, 4), generator=g, dtype=torch.int32)
