@@ -437,15 +437,16 @@ def cold_hbm_kernels(ext, wl, scratch, reps=10):
 
 def copy_ceiling(ext, scratch, reps=10):
     """The library's streaming copy (nt_stream_copy), cold, at about the
-    bytes the HBM kernels move (C2: 95 and 158 MB, C4: 400 MB, C5: 2.4 GB):
+    bytes the HBM kernels move (C1: 25 and 42 MB, C2: 95 and 158 MB, C4:
+    400 MB, C5: 2.4 GB):
     GB/s of bytes read + written. Short copies do not reach the long ones'
     rate (launch fill and drain), so each kernel compares with its size.
     Beside it, at the same byte counts, the write-only fill (nt_stream_fill:
     the ceiling of a kernel that mostly writes, like the dispatch's k copies
     of each row) and the read-only pass (nt_stream_read)."""
     out = {}
-    for label, moved in (("moved_95MB", 95e6), ("moved_158MB", 158e6), ("moved_400MB", 400e6),
-                         ("moved_2400MB", 2400e6)):
+    for label, moved in (("moved_25MB", 25e6), ("moved_42MB", 42e6), ("moved_95MB", 95e6),
+                         ("moved_158MB", 158e6), ("moved_400MB", 400e6), ("moved_2400MB", 2400e6)):
         n = int(moved // 2) // 16 * 16
         src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
