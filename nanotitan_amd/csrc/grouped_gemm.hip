@@ -2114,11 +2114,15 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
 // waves (measured: C4 +5%, C2 down-projection -10 us; shorter reductions and
 // the GELU epilogue were slower split).
 constexpr int64_t kSplitMinRed = 1024;
-// GELU forward with split duties only for long reductions (measured on
-// routed inputs, bit-identical either way: C4 up-projection, K = 4096,
-// 3885 -> 3840 us; C2, K = 512, 199 -> 282 us, where the short k-loop
-// cannot hide the storer waves' doubled store rounds).
-bool gelu_split(int64_t red) { return red >= 2048; }
+// GELU forward with split duties only for long reductions and the bf16
+// table (measured on routed inputs, bit-identical either way: C4
+// up-projection, K = 4096, 3885 -> 3840 us; C2, K = 512, 199 -> 282 us,
+// where the short k-loop cannot hide the storer waves' doubled store
+// rounds). fp16 evaluates gelu through the erfc fit, about four times the
+// table's VALU work per element; on half the waves that work outlasts the
+// next tile's loads (C5 up-projection, K = 2048: 2568-2593 us split,
+// 2105-2118 us with every wave in the epilogue).
+bool gelu_split(int dtype, int64_t red) { return dtype == NT_BF16 && red >= 2048; }
 template <int MODE, int EPI>
 int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   const int64_t chunks = g.chunk > 0 ? g.E + g.A / g.chunk : g.E;
@@ -2138,7 +2142,7 @@ int launch_mfma_auto(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
           return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2, true>(dtype, g, out_cols, s);
       }
       if constexpr (MODE == kFwd && EPI == kEpiGelu) {
-        if (gelu_split(g.K))
+        if (gelu_split(dtype, g.K))
           return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2, true>(dtype, g, out_cols, s);
       }
       return launch_mfma<MODE, EPI, 256, 256, 2, 4, 64, 2>(dtype, g, out_cols, s);
