@@ -359,14 +359,17 @@ pack_rows_kernel(const V* __restrict__ X, const float* __restrict__ w,
     }
   }
   if (sizeof(V) == 16 && k <= kSlotRegs) {
-    // 8 vectors per lane per batch from rows of 8 KiB, 4 below (one batch
-    // covers a 4 KiB row)
+    // 8 vectors per lane per batch from rows of 4 KiB up, 4 for rows up to
+    // 4 KiB, 2 for rows up to 2 KiB (one batch covers the row; fewer
+    // vectors would issue loads that only repeat the first)
     for (int t = wave; t < ntok; t += kDispatchWaves) {
-      if (nv >= (int64_t)kWave * kLongRowBatch)
-        copy_row_to_slot_regs<V, kLongRowBatch>(X + (tok0 + t) * nv, packed_X, nv, s_pos + t * k, k);
+      const V* src = X + (tok0 + t) * nv;
+      if (nv > (int64_t)kWave * kLongRowBatch / 2)
+        copy_row_to_slot_regs<V, kLongRowBatch>(src, packed_X, nv, s_pos + t * k, k);
+      else if (nv > (int64_t)kWave * kLongRowBatch / 4)
+        copy_row_to_slot_regs<V, kLongRowBatch / 2>(src, packed_X, nv, s_pos + t * k, k);
       else
-        copy_row_to_slot_regs<V, kLongRowBatch / 2>(X + (tok0 + t) * nv, packed_X, nv,
-                                                     s_pos + t * k, k);
+        copy_row_to_slot_regs<V, kLongRowBatch / 4>(src, packed_X, nv, s_pos + t * k, k);
     }
     return;
   }
