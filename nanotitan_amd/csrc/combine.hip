@@ -928,8 +928,9 @@ int run_combine_bwd_inv(const void* y, const int32_t* inv, const float* w, const
     }
   } else {
     // Short rows, k > 2: four rows per pass over dY (a second pass re-reads
-    // the token's dY row from L2) keeps the kernel at 71 registers instead
-    // of 95 (measured cold, C3: 126 -> 108 us; long rows were 5% slower so).
+    // the token's dY row from L2) keeps the kernel at 60 registers against
+    // 75 with all eight (measured cold, C3: 126 -> 108 us before the row
+    // loads were batched; long rows were 5% slower so).
     switch (ve) {
       case 8: NT_CBI(8, 4, 1); break;
       case 4: NT_CBI(4, 4, 1); break;
