@@ -2094,16 +2094,21 @@ int launch_mfma(int dtype, GemmArgs g, int64_t out_cols, hipStream_t s) {
   }
   constexpr int threads = WGM * WGN * kWave;
   auto kb = gg_mfma_kernel<bf16, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>;
-  auto kh = gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>;
   // Occupancy of this instantiation (bf16 and fp16 share resource usage).
   static const int per_cu = blocks_per_cu(kb, threads);
   // Persistent: at most one resident wave of workgroups; each walks tiles.
   const int64_t nblocks = std::min<int64_t>(tiles, (int64_t)device_cus(s) * per_cu);
   const dim3 grid((unsigned)nblocks);
-  if (dtype == NT_BF16)
+  if (dtype == NT_BF16) {
     hipLaunchKernelGGL(kb, grid, dim3(threads), 0, s, g);
-  else
-    hipLaunchKernelGGL(kh, grid, dim3(threads), 0, s, g);
+  } else if constexpr (EPI == kEpiGelu && SPLIT) {
+    // The GELU forward runs split only in bf16 (gelu_split), so no fp16 form
+    // of it is built.
+    return NT_ERR_DTYPE;
+  } else {
+    hipLaunchKernelGGL((gg_mfma_kernel<f16, MODE, BM, BN, WGM, WGN, BK, NS, EPI, SPLIT>), grid,
+                       dim3(threads), 0, s, g);
+  }
   return launch_status();
 }
 
