@@ -173,22 +173,40 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
+// The 16-bit GEMMs run on v_mfma_f32_16x16x32: the same operand registers
+// (8 elements per lane) and flops per register as 32x32x16, at lower power
+// per flop. The GPU holds its power limit by lowering the clock, so this
+// raises the sustained rate (measured on MI355X, MFMA chains from registers:
+// 1,916-1,922 TF/s at 1.92 GHz against 1,660-1,681 at 1.64-1.67 GHz; this
+// kernel's k-step with operands from LDS: 1,422-1,441 against 1,342-1,360;
+// the GEMMs, outputs bit-identical: C4 forward 1,171 -> 1,245 TF/s, dX
+// 1,120 -> 1,198, dW 1,090 -> 1,140, C2 layer step 1.028 -> 0.964 ms).
 template <typename T>
 struct mfma_op;
 template <>
 struct mfma_op<bf16> {
   typedef bf16x8_t vec;
-  __device__ static f32x16_t run(vec a, vec b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  __device__ static f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 template <>
 struct mfma_op<f16> {
   typedef f16x8_t vec;
-  __device__ static f32x16_t run(vec a, vec b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  __device__ static f32x4_t run(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
+
+// Accumulators of one wave: acc[i][j][g] holds 16x16 block g of the 32x32
+// sub-tile (i, j) of the wave's output block, with the B fragment issued as
+// the MFMA's first operand, so that lane l, element q holds
+//   C[32 i + acc_row(g, l)][32 j + acc_col(g, l) + q]:
+// 4 consecutive output columns of one row per block.
+template <int TM, int TN>
+using AccTile = f32x4_t[TM][TN][4];
+__device__ __forceinline__ int acc_row(int g, int lane) { return 16 * (g >> 1) + (lane & 15); }
+__device__ __forceinline__ int acc_col(int g, int lane) { return 16 * (g & 1) + 4 * (lane >> 4); }
 
 // Two fp32 values rounded to nearest-even and packed into 32 bits (first
 // value in the low half). bf16 uses the hardware pair conversion
@@ -310,17 +328,21 @@ __device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t r, uint32_t off, 
 // r..r+15, one chunk) then touches all 64 banks once.
 //
 // MN-major (m / n contiguous in HBM): row k of the tile holds ROWS elements
-// (ROWS/8 chunks), chunk c stored at c ^ (4 * (k & 3)). Fragments come from
+// (ROWS/8 chunks), chunk c stored at c ^ mn_swizzle(k). Fragments come from
 // ds_read_b64_tr_b16, which transposes 4x4 blocks of 16-bit elements across
 // each 16-lane group: source lane 4j+q reads the 4 elements at (k0 + j,
 // mn0 + 4q .. 4q+3); destination lane 4q+e receives (k0 + 0..3, mn0 + 4q + e).
 // Two such reads (k0 and k0 + 4) give a lane the 8 consecutive reduction
-// elements of one m / n index that v_mfma_f32_32x32x16 takes. 32 lanes per
-// LDS cycle read 4 rows x 4 chunks, which the XOR spreads over all 64 banks.
+// elements of one m / n index that v_mfma_f32_16x16x32 takes; lane group g
+// reads rows 8g .. 8g+7 of the substep. 32 lanes per LDS cycle (groups 0
+// and 1, or 2 and 3) read rows k0 + 0..3 and k0 + 8..11, two chunks each;
+// the XOR (bits 0, 1 and 3 of k) places those 16 chunks on all 64 banks.
 //
-// Wave w issues instructions w, w+8, ...; for a given lane these differ only
-// by a whole number of XOR periods, so one per-lane offset plus a uniform
-// stride per instruction covers them.
+// Wave w issues instructions w, w+NW, ...; where the rows of successive
+// instructions differ by a whole number of XOR periods (16 rows), one
+// per-lane offset plus a uniform stride per instruction covers them, else
+// two offsets (even and odd instructions).
+__device__ __forceinline__ int mn_swizzle(int k) { return 4 * (k & 3) + 2 * ((k >> 3) & 1); }
 template <int ROWS, bool KMAJ, int BK, int NW>
 struct OperandTile {
   static_assert(BK == 32 || BK == 64, "k-step of 32 or 64 elements");
@@ -333,17 +355,27 @@ struct OperandTile {
   static constexpr int kRowsPerInst = 1024 / kRowBytes;
   static constexpr int kCpr = KMAJ ? BK / 8 : ROWS / 8;  // chunks per row
   static constexpr int kRpw = 16 / (BK / 8);             // K-major rows per bank sweep
+  static constexpr int kStepRows = NW * kRowsPerInst;    // rows between a wave's instructions
+  static constexpr bool kTwo = !KMAJ && kStepRows % 16 != 0;
+  static_assert(KMAJ || kStepRows % 8 == 0, "MN-major swizzle: 8-row steps");
+  static_assert(!kTwo || kPer % 2 == 0, "MN-major swizzle: even instruction count");
 
   uint32_t off;     // byte offset of this lane's chunk (instruction `wave`) from the tile origin
+  uint32_t off2;    // kTwo: the same for instruction `wave` + NW
   uint32_t kchunk;  // K-major: first reduction index of the lane's chunk
-  uint32_t ustep;   // byte stride between this wave's successive instructions
+  uint32_t ustep;   // byte stride between this wave's successive instructions (kTwo: of
+                    // every second one)
 
   __device__ void init(int64_t ld, int wave, int lane) {
     const int r = kRowsPerInst * wave + lane / kCpr;
-    const int c = KMAJ ? (lane % kCpr) ^ ((r / kRpw) % kCpr) : (lane % kCpr) ^ (4 * (r & 3));
+    const int c = KMAJ ? (lane % kCpr) ^ ((r / kRpw) % kCpr) : (lane % kCpr) ^ mn_swizzle(r);
     off = (uint32_t)((int64_t)r * ld + c * 8) * 2u;
     kchunk = (uint32_t)(c * 8);
-    ustep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(NW * kRowsPerInst * ld * 2));
+    if (kTwo) {
+      const int r2 = r + kStepRows;
+      off2 = (uint32_t)((int64_t)r2 * ld + ((lane % kCpr) ^ mn_swizzle(r2)) * 8) * 2u;
+    }
+    ustep = (uint32_t)__builtin_amdgcn_readfirstlane((int)((kTwo ? 2 : 1) * kStepRows * ld * 2));
   }
 
   // Issue this wave's share of the tile's loads. `base` is the tile origin
@@ -358,38 +390,55 @@ struct OperandTile {
     // Instruction u reads u * ustep bytes further on. The offset advances
     // through an opaque add, so the compiler keeps one offset register
     // instead of hoisting kPer of them out of the k-loop.
+    if constexpr (kTwo) {
+      uint32_t v2 = off2;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      load16_to_lds(rs, v, __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
-      if (u + 1 < kPer) v = add_opaque(v, ustep);
+      for (int u = 0; u < kPer; u += 2) {
+        load16_to_lds(rs, v, __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
+        load16_to_lds(rs, v2, __builtin_amdgcn_readfirstlane(l0 + (uint32_t)((u + 1) * NW * 1024)));
+        if (u + 2 < kPer) {
+          v = add_opaque(v, ustep);
+          v2 = add_opaque(v2, ustep);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        load16_to_lds(rs, v, __builtin_amdgcn_readfirstlane(l0 + (uint32_t)(u * NW * 1024)));
+        if (u + 1 < kPer) v = add_opaque(v, ustep);
+      }
     }
   }
 };
 
-// Per-lane LDS byte offsets of the fragment reads of one operand: TS 32-row
-// sub-tiles starting at row `row0` of the tile, for each of the BK/16
-// k-substeps of 16 elements.
+// Per-lane LDS byte offsets of the fragment reads of one operand: TS 16-row
+// blocks starting at row `row0` of the tile, for each of the BK/32
+// k-substeps of 32 elements. Lane l supplies index l % 16 of a block and
+// reduction elements 8 (l / 16) .. +7 of the substep.
 template <int ROWS, bool KMAJ, int TS, int BK>
 struct FragReader {
   static constexpr int kRowBytes = KMAJ ? BK * 2 : ROWS * 2;
   static constexpr int kCpr = BK / 8;
   static constexpr int kRpw = 16 / kCpr;
-  uint32_t base[KMAJ ? BK / 16 : TS];
+  uint32_t base[KMAJ ? BK / 32 : TS];
   __device__ void init(int row0, int lane) {
     if (KMAJ) {
-      const int r = row0 + (lane & 31);
+      // the K-major XOR repeats every 16 rows, so blocks differ by a stride
+      const int r = row0 + (lane & 15);
 #pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        const int c = (2 * ks + (lane >> 5)) ^ ((r / kRpw) % kCpr);
+      for (int ks = 0; ks < BK / 32; ++ks) {
+        const int c = (4 * ks + (lane >> 4)) ^ ((r / kRpw) % kCpr);
         base[ks] = (uint32_t)(r * kRowBytes + c * 16);
       }
     } else {
+      // mn_swizzle repeats every 16 rows and ignores bit 2, so the substep
+      // (32 rows on) and the second read (4 rows on) are strides
       const int g = lane >> 4, s = lane & 15, j = s >> 2, q = s & 3;
-      const int k = 8 * (g >> 1) + j;
+      const int k = 8 * g + j;
 #pragma unroll
       for (int t = 0; t < TS; ++t) {
-        const int mn = row0 + 32 * t + 16 * (g & 1) + 4 * q;
-        const int c = (mn >> 3) ^ (4 * (k & 3));
+        const int mn = row0 + 16 * t + 4 * q;
+        const int c = (mn >> 3) ^ mn_swizzle(k);
         base[t] = (uint32_t)(k * kRowBytes + c * 16 + (mn & 7) * 2);
       }
     }
@@ -397,9 +446,9 @@ struct FragReader {
   template <typename V>
   __device__ V read(const char* lds, int t, int ks) const {
     if (KMAJ) {
-      return *reinterpret_cast<const V*>(lds + base[ks] + t * 32 * kRowBytes);
+      return *reinterpret_cast<const V*>(lds + base[ks] + t * 16 * kRowBytes);
     } else {
-      const char* p = lds + base[t] + 16 * ks * kRowBytes;
+      const char* p = lds + base[t] + 32 * ks * kRowBytes;
       const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
       const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * kRowBytes));
       const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -730,29 +779,29 @@ struct StageLoader {
   }
 };
 
-// Epilogue: acc[i][j][v] = C[m][n] with m = m0 + 32i + lane%32 and
-// n = n0 + 32j + 8*(v/4) + 4*(lane/32) + v%4; each lane stores 4
-// consecutive columns (8 bytes) per group, rounded once (RNE).
+// Epilogue straight from the accumulators (AccTile layout): each lane
+// stores 4 consecutive columns (8 bytes) per block, rounded once (RNE).
 template <typename T, int TM, int TN>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[TM][TN], const TileJob& j, int m0,
+__device__ __forceinline__ void store_tile(const AccTile<TM, TN>& acc, const TileJob& j, int m0,
                                            int n0, int lane) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + i * 32 + (lane & 31);
-    if (m >= j.rows_valid) continue;
-    uint16_t* prow = j.po + (int64_t)m * j.ldo;
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int jn = 0; jn < TN; ++jn)
+    for (int gq = 0; gq < 4; ++gq) {
+      const int m = m0 + i * 32 + acc_row(gq, lane);
+      if (m >= j.rows_valid) continue;
+      uint16_t* prow = j.po + (int64_t)m * j.ldo;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + jn * 32 + 8 * gq + 4 * (lane >> 5);
+      for (int jn = 0; jn < TN; ++jn) {
+        const int n = n0 + jn * 32 + acc_col(gq, lane);
         if (n >= j.cols_valid) continue;
+        const f32x4_t& a = acc[i][jn][gq];
         uint2 pk;
-        pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
-        pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
+        pk.x = pack2<T>(a[0], a[1]);
+        pk.y = pack2<T>(a[2], a[3]);
         *reinterpret_cast<uint2*>(prow + n) = pk;
       }
-  }
+    }
 }
 
 // GELU, erf form, for 16-bit outputs: gelu(x) = x * Phi(x) and
@@ -929,16 +978,16 @@ __device__ __forceinline__ void epilogue8(uint4 v, __amdgpu_buffer_rsrc_t ro,
 
 // Epilogue through LDS for 64- or 128-column wave blocks (TN = 2 or 4):
 // each 32-row sub-tile is rounded (RNE), written to this wave's LDS scratch
-// (pitch 32*TN*2 + 8 bytes: the 8-byte writes of 32 rows fall on distinct
-// banks), and read back 16 bytes per lane so that every store instruction
-// writes whole 128- or 256-byte row segments. `scratch` is
-// epi_bytes<TN, ROWS>() bytes private to the wave; LDS operations of one
-// wave complete in order, so no barrier is needed (a wavefront fence keeps
-// the compiler from reusing a lane's earlier reads). With ROWS = 16 the
-// sub-tile goes through in two halves (lanes 0-15 and 32-47 hold rows 0-15,
-// the others rows 16-31), halving the scratch.
+// (pitch 32*TN*2 + 16 bytes: one 8-byte write instruction covers 16 rows x
+// 16 bytes, which then fall on distinct banks), and read back 16 bytes per
+// lane so that every store instruction writes whole 128- or 256-byte row
+// segments. `scratch` is epi_bytes<TN, ROWS>() bytes private to the wave;
+// LDS operations of one wave complete in order, so no barrier is needed (a
+// wavefront fence keeps the compiler from reusing a lane's earlier reads).
+// With ROWS = 16 the sub-tile goes through in two halves (blocks 0, 1 hold
+// rows 0-15, blocks 2, 3 rows 16-31), halving the scratch.
 template <int TN>
-constexpr int epi_pitch() { return 64 * TN + 8; }
+constexpr int epi_pitch() { return 64 * TN + 16; }
 template <int TN, int ROWS>
 constexpr int epi_bytes() { return ROWS * epi_pitch<TN>(); }
 // Store instructions one wave issues in store_tile_lds.
@@ -948,7 +997,7 @@ constexpr int epi_stores() {
          (EPI == kEpiGelu || EPI == kEpiSwiGLUGrad ? 2 : 1);
 }
 template <typename T, int EPI, bool TAB, int ROWS, int TM, int TN>
-__device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+__device__ __forceinline__ void store_tile_lds(const AccTile<TM, TN>& acc, const TileJob& j,
                                                int m0, int n0, int lane, char* scratch,
                                                const uint32_t* tab) {
   static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
@@ -994,27 +1043,25 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
-      const int r = lane & 31;
-      const bool mine = kPasses == 1 || (r / ROWS) == ps;
-      if (mine) {
+      // the blocks of this pass's rows: all four, or blocks 2 ps and 2 ps + 1
 #pragma unroll
-        for (int jn = 0; jn < TN; ++jn)
+      for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
-            uint2 pk;
-            pk.x = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
-            pk.y = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
-            *reinterpret_cast<uint2*>(scratch + (r % ROWS) * kPitch + c * 2) = pk;
-          }
-      }
+        for (int h = 0; h < 4 / kPasses; ++h) {
+          const int gq = ps * (4 / kPasses) + h;
+          const int c = jn * 32 + acc_col(gq, lane);
+          const f32x4_t& a = acc[i][jn][gq];
+          uint2 pk;
+          pk.x = pack2<T>(a[0], a[1]);
+          pk.y = pack2<T>(a[2], a[3]);
+          *reinterpret_cast<uint2*>(scratch + (acc_row(gq, lane) % ROWS) * kPitch + c * 2) = pk;
+        }
       // Each lane reads back rows other lanes wrote. The compiler models
       // lanes as threads, so without a fence it may forward a lane's earlier
-      // read of the same scratch address where that lane wrote nothing: with
-      // 16-row passes it moved the second pass's reads into the writing
-      // lanes' branch, and the other lanes stored the first pass's rows
-      // again. A wavefront-scope fence emits no instruction (a wave's LDS
-      // operations complete in order) and forbids that.
+      // read of the same scratch address where that lane wrote nothing (it
+      // did so where only some lanes wrote each pass). A wavefront-scope
+      // fence emits no instruction (a wave's LDS operations complete in
+      // order) and forbids that.
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       auto chunk_off = [&](int q, uint4& v) -> uint32_t {
         const int rr = q * kRowsPerRead + lane / kLanesPerRow;
@@ -1079,7 +1126,7 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[TM][TN], co
 //
 // Rows per round: whole 32-row sub-tiles where eight waves' regions fit in
 // the idle 64 KiB stage (plain and two-part epilogues on 64-column wave
-// blocks: 34 KiB), halving the rounds and their barriers; 16-row halves for
+// blocks: 36 KiB), halving the rounds and their barriers; 16-row halves for
 // the GELU epilogue's two regions and 128-column wave blocks. Measured on
 // MI355X, bit-identical: C2 layer step 0.9947 -> 0.9879 ms (mean of four
 // alternations), C4 level.
@@ -1091,7 +1138,7 @@ constexpr int split_scratch_bytes(int nw) {
 }
 template <typename T, int TM, int TN, int WGN, int WM, int WN, int NW, int EPI = kEpiPlain,
           bool TAB = false>
-__device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+__device__ __forceinline__ void store_tile_split(const AccTile<TM, TN>& acc, const TileJob& j,
                                                  int wave, int lane, char* scratch,
                                                  const uint32_t* tab = nullptr) {
   static_assert(TN == 2 || TN == 4, "64- or 128-column wave blocks");
@@ -1114,49 +1161,53 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
   char* mine = scratch + wave * kRegion;
   const __amdgpu_buffer_rsrc_t ro = out_rsrc(j.po);
   const __amdgpu_buffer_rsrc_t ro2 = out_rsrc(kGelu ? j.po2 : j.po);
-  const int r = lane & 31;
+  constexpr int kG = ROWS / 8;  // 16x16 blocks per 32-column block in one round
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int ps = 0; ps < 32 / ROWS; ++ps) {
-      if (r / ROWS == ps) {
-        char* row = mine + (r % ROWS) * kPitch;
-        uint32_t w[2 * TN * 4];
+      // blocks ps kG .. ps kG + kG - 1 of each column block: every lane
+      // holds 4 kG values of a row of this round per column block
+      uint32_t w[2 * TN * kG];
+#pragma unroll
+      for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+        for (int h = 0; h < kG; ++h) {
+          const f32x4_t& a = acc[i][jn][ps * kG + h];
+          w[2 * (kG * jn + h)] = pack2<T>(a[0], a[1]);
+          w[2 * (kG * jn + h) + 1] = pack2<T>(a[2], a[3]);
+        }
+      auto put = [&](int jn, int h, char* region, uint32_t lo, uint32_t hi) {
+        const int gq = ps * kG + h;
+        const int c = jn * 32 + acc_col(gq, lane);
+        *reinterpret_cast<uint2*>(region + (acc_row(gq, lane) % ROWS) * kPitch + c * 2) =
+            make_uint2(lo, hi);
+      };
+      if constexpr (kGelu) {
+        // gelu and gelu' of the rounded h (h itself is not stored)
+        uint32_t g1[2 * TN * kG], g2[2 * TN * kG];
+        if constexpr (TAB) {
+          gelu_table<2 * TN * kG>(w, tab, g1, g2);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 2 * TN * kG; ++q) gelu2_formula<T>(w[q], g1[q], g2[q]);
+        }
 #pragma unroll
         for (int jn = 0; jn < TN; ++jn)
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            w[2 * (4 * jn + gq)] = pack2<T>(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1]);
-            w[2 * (4 * jn + gq) + 1] = pack2<T>(acc[i][jn][4 * gq + 2], acc[i][jn][4 * gq + 3]);
+          for (int h = 0; h < kG; ++h) {
+            const int q = kG * jn + h;
+            put(jn, h, mine, g1[2 * q], g1[2 * q + 1]);
+            put(jn, h, mine + kOut2, g2[2 * q], g2[2 * q + 1]);
           }
-        if constexpr (kGelu) {
-          // gelu and gelu' of the rounded h (h itself is not stored)
-          uint32_t g1[2 * TN * 4], g2[2 * TN * 4];
-          if constexpr (TAB) {
-            gelu_table<2 * TN * 4>(w, tab, g1, g2);
-          } else {
+      } else {
 #pragma unroll
-            for (int q = 0; q < 2 * TN * 4; ++q) gelu2_formula<T>(w[q], g1[q], g2[q]);
+        for (int jn = 0; jn < TN; ++jn)
+#pragma unroll
+          for (int h = 0; h < kG; ++h) {
+            const int q = kG * jn + h;
+            put(jn, h, mine, w[2 * q], w[2 * q + 1]);
           }
-#pragma unroll
-          for (int jn = 0; jn < TN; ++jn)
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-              const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
-              const int q = 4 * jn + gq;
-              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(g1[2 * q], g1[2 * q + 1]);
-              *reinterpret_cast<uint2*>(row + kOut2 + c * 2) = make_uint2(g2[2 * q], g2[2 * q + 1]);
-            }
-        } else {
-#pragma unroll
-          for (int jn = 0; jn < TN; ++jn)
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-              const int c = jn * 32 + 8 * gq + 4 * (lane >> 5);
-              const int q = 4 * jn + gq;
-              *reinterpret_cast<uint2*>(row + c * 2) = make_uint2(w[2 * q], w[2 * q + 1]);
-            }
-        }
       }
       __syncthreads();
       if (storer) {
@@ -1188,41 +1239,57 @@ __device__ __forceinline__ void store_tile_split(const f32x16_t (&acc)[TM][TN], 
 // fp32 partial of a split dW tile: each lane stores its 4 consecutive
 // columns of a row as one 16-byte write; the reduce pass rounds later.
 template <int TM, int TN>
-__device__ __forceinline__ void store_partial(const f32x16_t (&acc)[TM][TN], const TileJob& j,
+__device__ __forceinline__ void store_partial(const AccTile<TM, TN>& acc, const TileJob& j,
                                               int m0, int n0, int lane) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int m = m0 + i * 32 + (lane & 31);
-    if (m >= j.rows_valid) continue;
-    float* prow = j.pf + (int64_t)m * j.ldo;
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int jn = 0; jn < TN; ++jn)
+    for (int gq = 0; gq < 4; ++gq) {
+      const int m = m0 + i * 32 + acc_row(gq, lane);
+      if (m >= j.rows_valid) continue;
+      float* prow = j.pf + (int64_t)m * j.ldo;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + jn * 32 + 8 * gq + 4 * (lane >> 5);
+      for (int jn = 0; jn < TN; ++jn) {
+        const int n = n0 + jn * 32 + acc_col(gq, lane);
         if (n >= j.cols_valid) continue;
-        *reinterpret_cast<float4*>(prow + n) =
-            make_float4(acc[i][jn][4 * gq + 0], acc[i][jn][4 * gq + 1], acc[i][jn][4 * gq + 2],
-                        acc[i][jn][4 * gq + 3]);
+        const f32x4_t& a = acc[i][jn][gq];
+        *reinterpret_cast<float4*>(prow + n) = make_float4(a[0], a[1], a[2], a[3]);
       }
-  }
+    }
 }
 
+// On 128-register wave tiles every accumulator register is zeroed by an
+// instruction of its own that the compiler cannot see through. With a
+// literal (or one shared) zero it specialises the peeled first k-step into
+// MFMAs on a common zero operand whose results land in other registers than
+// the loop's, and the reshuffle took those kernels to 256 registers and
+// spills. Smaller tiles keep their accumulators in AGPRs, where the opaque
+// (VGPR) zeros cost more than they save.
+__device__ __forceinline__ float opaque_zero() {
+  float z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
 template <typename T, int TM, int TN>
-__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[TM][TN]) {
+__device__ __forceinline__ void zero_acc(AccTile<TM, TN>& acc) {
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+      for (int g = 0; g < 4; ++g) {
+        if constexpr (TM * TN >= 8)
+          acc[i][j][g] = f32x4_t{opaque_zero(), opaque_zero(), opaque_zero(), opaque_zero()};
+        else
+          acc[i][j][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
 }
 
 // Persistent grouped GEMM. Each workgroup of WGM x WGN waves walks a range
 // of BM x BN output tiles; each wave owns a (BM/WGM) x (BN/WGN) block of
-// 32x32 MFMA tiles. The MFMA is issued with the B fragment as its first
-// operand, so each lane's accumulator holds 4 consecutive output columns of
-// one output row. K advances BK per iteration through a ring of NS LDS
+// 16x16 MFMA blocks (AccTile). The MFMA is issued with the B fragment as its
+// first operand, so each lane's accumulator holds 4 consecutive output
+// columns of one output row. K advances BK per iteration through a ring of NS LDS
 // stages: the loads of stage kt+NS-1 are issued right after the barrier of
 // iteration kt and have NS-1 iterations of MFMAs to land. The first stages
 // of a workgroup's next tile are issued before the current tile's results
@@ -1422,8 +1489,10 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   // of the same outputs.
   constexpr int kBRows = kDual == 1 ? BN / 2 : BN;
   constexpr int kBTs = kDual == 1 ? TN / 2 : TN;
-  FragReader<BM, kAK, TM, BK> fa;
-  FragReader<kBRows, kBKm, kBTs, BK> fb;
+  constexpr int kAB = 2 * TM, kBB = 2 * TN;  // 16-row A and 16-column B blocks
+  constexpr int kKS = BK / 32;               // 32-deep substeps per k-step
+  FragReader<BM, kAK, kAB, BK> fa;
+  FragReader<kBRows, kBKm, 2 * kBTs, BK> fb;
   fa.init(wm * WM, lane);
   fb.init(wn * (WN * kBRows / BN), lane);
 
@@ -1440,36 +1509,49 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
   }
 
   typedef typename mfma_op<T>::vec vec;
-  f32x16_t acc[TM][TN];
-  // Fragments for substep ks+1 are read (into the other register set)
-  // before the MFMAs of ks are issued; scheduling fences keep that order, so
-  // the LDS latency of ks+1 hides behind the MFMAs of ks.
+  AccTile<TM, TN> acc;
+  // The operand with fewer blocks per wave ("held") is read a substep ahead
+  // into a second register set; the other one streams, each block read two
+  // blocks ahead of its MFMAs, across the substeps of the k-step (3 blocks
+  // of registers instead of 2 x 2 TM). Scheduling fences keep that order, so
+  // the LDS latency hides behind the MFMAs of the blocks before.
+  constexpr bool kStreamA = TM >= TN;
+  constexpr int kHeld = kStreamA ? kBB : kAB;
+  constexpr int kStr = kStreamA ? kAB : kBB;
   auto compute = [&](const char* sa, const char* sb) {
-    vec av[2][TM], bv[2][TN];
-    auto read_b = [&](int j, int ks) {
-      if (kDual == 1 && j >= kBTs)
-        return fb.template read<vec>(sb + Loader::TB::kBytes, j - kBTs, ks);
-      return fb.template read<vec>(sb, j, ks);
+    auto read_a = [&](int ib, int ks) { return fa.template read<vec>(sa, ib, ks); };
+    auto read_b = [&](int jb, int ks) {
+      if (kDual == 1 && jb >= 2 * kBTs)
+        return fb.template read<vec>(sb + Loader::TB::kBytes, jb - 2 * kBTs, ks);
+      return fb.template read<vec>(sb, jb, ks);
     };
+    auto read_held = [&](int h, int ks) { return kStreamA ? read_b(h, ks) : read_a(h, ks); };
+    auto read_str = [&](int n) {
+      return kStreamA ? read_a(n % kStr, n / kStr) : read_b(n % kStr, n / kStr);
+    };
+    vec held[2][kHeld];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) av[0][i] = fa.template read<vec>(sa, i, 0);
+    for (int h = 0; h < kHeld; ++h) held[0][h] = read_held(h, 0);
+    vec s0 = read_str(0), s1 = read_str(1);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) bv[0][j] = read_b(j, 0);
+    for (int n = 0; n < kKS * kStr; ++n) {
+      const int ks = n / kStr, x = n % kStr, cur = ks & 1;
+      if (x == 0 && ks + 1 < kKS) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < BK / 16) {
+        for (int h = 0; h < kHeld; ++h) held[cur ^ 1][h] = read_held(h, ks + 1);
+      }
+      vec s2 = s1;
+      if (n + 2 < kKS * kStr) s2 = read_str(n + 2);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) av[cur ^ 1][i] = fa.template read<vec>(sa, i, ks + 1);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bv[cur ^ 1][j] = read_b(j, ks + 1);
+      for (int h = 0; h < kHeld; ++h) {
+        const int ib = kStreamA ? x : h, jb = kStreamA ? h : x;
+        f32x4_t& c = acc[ib >> 1][jb >> 1][2 * (ib & 1) + (jb & 1)];
+        c = kStreamA ? mfma_op<T>::run(held[cur][h], s0, c) : mfma_op<T>::run(s0, held[cur][h], c);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_op<T>::run(bv[cur][j], av[cur][i], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
+      s0 = s1;
+      s1 = s2;
     }
   };
 
@@ -1565,24 +1647,28 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
       static_assert(NW * epi_bytes<TNO, kRows>() <= kStage, "epilogue scratch fits one stage");
       char* scr = smem + (NS - 1) * kStage + wave * epi_bytes<TNO, kRows>();
       const int n0 = wn * (WN / 2);
-      f32x16_t part[TM][TNO];
+      AccTile<TM, TNO> part;
       TileJob jo = job;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int jn = 0; jn < TNO; ++jn)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            acc[i][jn][v] = round_to<T>(acc[i][jn][v]);
-            acc[i][jn + TNO][v] = round_to<T>(acc[i][jn + TNO][v]);
-            part[i][jn][v] = acc[i][jn][v];
-          }
+          for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              acc[i][jn][gq][v] = round_to<T>(acc[i][jn][gq][v]);
+              acc[i][jn + TNO][gq][v] = round_to<T>(acc[i][jn + TNO][gq][v]);
+              part[i][jn][gq][v] = acc[i][jn][gq][v];
+            }
       jo.po = job.po2;
       store_tile_lds<T, kEpiPlain, false, kRows>(part, jo, wm * WM, n0, lane, scr, s_gtab);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int jn = 0; jn < TNO; ++jn) part[i][jn] = acc[i][jn + TNO];
+        for (int jn = 0; jn < TNO; ++jn)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) part[i][jn][gq] = acc[i][jn + TNO][gq];
       jo.po = job.po3;
       store_tile_lds<T, kEpiPlain, false, kRows>(part, jo, wm * WM, n0, lane, scr, s_gtab);
 #pragma unroll
@@ -1590,8 +1676,10 @@ __device__ __forceinline__ void gemm_tiles(const GemmArgs& g, int64_t wg, int64_
 #pragma unroll
         for (int jn = 0; jn < TNO; ++jn)
 #pragma unroll
-          for (int v = 0; v < 16; ++v)
-            part[i][jn][v] = swiglu_hidden<T>(acc[i][jn][v], acc[i][jn + TNO][v]);
+          for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              part[i][jn][gq][v] = swiglu_hidden<T>(acc[i][jn][gq][v], acc[i][jn + TNO][gq][v]);
       store_tile_lds<T, kEpiPlain, false, kRows>(part, job, wm * WM, n0, lane, scr, s_gtab);
       stores_out = kDrain && more;
     } else if constexpr (kSplit) {
