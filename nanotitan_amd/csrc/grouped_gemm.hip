@@ -990,6 +990,19 @@ template <int TN>
 constexpr int epi_pitch() { return 64 * TN + 16; }
 template <int TN, int ROWS>
 constexpr int epi_bytes() { return ROWS * epi_pitch<TN>(); }
+// Scratch row that `lane` reads back (16 bytes, chunk lane % (4 TN)) in
+// read instruction q. 64-column blocks: 8 lanes per 128-byte row, and the
+// two 8-lane halves of each 16-lane LDS cycle take rows 8 apart, which the
+// pitch puts 32 banks apart (rows r and r + 1 would share 4 banks, a
+// second pass for every read). 128-column blocks: 16 lanes read one whole
+// 256-byte row.
+template <int TN>
+__device__ __forceinline__ int epi_read_row(int q, int lane) {
+  if constexpr (TN == 2)
+    return (16 * (q >> 1) + (q & 1)) | (lane & 8) | ((lane >> 3) & 6);
+  else
+    return 4 * q + (lane >> 4);
+}
 // Store instructions one wave issues in store_tile_lds.
 template <int EPI, int ROWS, int TM, int TN>
 constexpr int epi_stores() {
@@ -1024,7 +1037,7 @@ __device__ __forceinline__ void store_tile_lds(const AccTile<TM, TN>& acc, const
   const __amdgpu_buffer_rsrc_t ra = out_rsrc(kAux ? j.paux : j.po);
   const __amdgpu_buffer_rsrc_t ra2 = out_rsrc(kAux2 ? j.paux2 : j.po);
   auto load_aux = [&](int i, int ps, int q) {
-    const int m = m0 + i * 32 + ps * ROWS + q * kRowsPerRead + lane / kLanesPerRow;
+    const int m = m0 + i * 32 + ps * ROWS + epi_read_row<TN>(q, lane);
     const int n = n0 + (lane % kLanesPerRow) * 8;
     const uint32_t off = (m < rv && n < cv) ? ((uint32_t)m * ldo + (uint32_t)n) * 2u : kOob;
     aux[ps * (ROWS / kRowsPerRead) + q] = load16(ra, off);
@@ -1064,7 +1077,7 @@ __device__ __forceinline__ void store_tile_lds(const AccTile<TM, TN>& acc, const
       // order) and forbids that.
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       auto chunk_off = [&](int q, uint4& v) -> uint32_t {
-        const int rr = q * kRowsPerRead + lane / kLanesPerRow;
+        const int rr = epi_read_row<TN>(q, lane);
         const int ch = lane % kLanesPerRow;
         v = *reinterpret_cast<const uint4*>(scratch + rr * kPitch + ch * 16);
         const int m = m0 + i * 32 + ps * ROWS + rr;
@@ -1219,7 +1232,7 @@ __device__ __forceinline__ void store_tile_split(const AccTile<TM, TN>& acc, con
           const char* sp = scratch + src * kRegion;
 #pragma unroll
           for (int q = 0; q < kQ; ++q) {
-            const int rr = q * kRowsPerRead + lane / kLanesPerRow;
+            const int rr = epi_read_row<TN>(q, lane);
             const int ch = lane % kLanesPerRow;
             const int m = sm0 + rr;
             const int n = sn0 + ch * 8;
