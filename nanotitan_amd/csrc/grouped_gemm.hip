@@ -2182,7 +2182,12 @@ int blocks_per_cu(K kernel, int threads) {
 // up-projection 226 -> 200 us, plain up-projection 163 -> 149 us, plain dX
 // (reduction 512) 165 -> 152 us, GELU dX 199 -> 185 us. Half or 1.5 times
 // this delay gained less, 3 times lost; at longer reductions or fewer tiles
-// the delay only lengthens the tail.
+// the delay only lengthens the tail. The GELU epilogues (table or gelu'
+// reads on top of the stores) with at least 6 tiles per CU take 1.5 times
+// the delay (measured on the 16x16x32 kernels, three alternations: C2
+// layer step 0.9333-0.9352 -> 0.9253-0.9283 ms, C3 and C5 level; 1.5 times
+// for every launch with 6 tiles per CU made C3 1% slower, 2 times was
+// slower at C2).
 int32_t stagger_ticks(int mode, int epi, int64_t red, int64_t tiles, int64_t cus, int BM, int BN) {
   if (mode == kDw || red > 1024 || tiles < 4 * cus) return 0;
   int tensors = 1;  // output tiles written plus input tiles read by the epilogue
@@ -2190,7 +2195,8 @@ int32_t stagger_ticks(int mode, int epi, int64_t red, int64_t tiles, int64_t cus
   if (epi == kEpiSwiGLU) tensors = 3;
   if (epi == kEpiSwiGLUGrad) tensors = 4;
   const int64_t bytes = (int64_t)tensors * BM * (epi == kEpiSwiGLU ? BN / 2 : BN) * 2 * cus;
-  return (int32_t)(bytes / 60000);  // bytes / 6 TB/s, in 10 ns ticks
+  const bool gelu_many = tensors == 2 && tiles >= 6 * cus;
+  return (int32_t)(bytes / 60000 * (gelu_many ? 3 : 2) / 2);  // bytes / 6 TB/s, in 10 ns ticks
 }
 
 template <int MODE, int EPI, int BM, int BN, int WGM, int WGN, int BK, int NS, bool SPLIT = false>
